@@ -1,0 +1,317 @@
+"""Benchmark of the paged-KV attention path on one MI355X.
+
+Default workload: Llama-3-8B-shape decode attention for one layer: 32 query
+heads, 8 kv heads, head_dim 128, one query token over 32,768 cached tokens
+(128 pages of 256), fp32 KV (the reference's page type), batch 1.  A step is
+one attention call over one batch; the KV of consecutive steps rotates
+through copies totalling more than 1 GB, so the 256 MB Infinity Cache cannot
+serve repeats.  Inputs are synthetic N(0,1) (RoPE at base 500000 on Q and K)
+generated on the device.
+
+Prints one JSON line (rank 0, N=1).  `value` is the achieved HBM throughput
+(algorithmic bytes per step / step time) in TB/s.  `roofline` is computed
+for the dominant kernel from HIP events around the timed steps.
+`cpu_baseline` times the oracle's op-order restatement of the reference's
+single-threaded Vector256 path on one host core over a bounded sample.
+
+Other workloads (--config): see WORKLOADS.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode attn µs/token & achieved HBM TB/s (% peak), 8B-shape @32K ctx, 1 GPU"
+HBM_PEAK_TBS = 8.0
+MFMA_PEAK_TFS = {"bf16": 2500.0, "f16": 2500.0}
+ROTATE_BYTES = 1.1e9
+
+WORKLOADS = {
+    # name: kind, heads, kv_heads, head_dim, cached tokens, kv dtype, batch, [queries]
+    "c1": dict(kind="decode", heads=8, kv=2, D=64, n=512, dtype="f32", B=1, rope=0.0,
+               desc="tiny GQA decode, 8 q heads / 2 kv heads / head_dim 64, 512 cached fp32 tokens, batch 1"),
+    "c2-f32-b1": dict(kind="decode", heads=32, kv=8, D=128, n=32768, dtype="f32", B=1, rope=500000.0,
+                      desc="llama-3-8b-shape decode attention, 32 q heads / 8 kv heads / head_dim 128, "
+                           "32768 cached tokens (128 pages), fp32 KV, batch 1"),
+    "c2-f16-b1": dict(kind="decode", heads=32, kv=8, D=128, n=32768, dtype="f16", B=1, rope=500000.0,
+                      desc="llama-3-8b-shape decode attention, 32768 cached tokens, fp16 KV, batch 1"),
+    "c2-f32-b16": dict(kind="decode", heads=32, kv=8, D=128, n=32768, dtype="f32", B=16, rope=500000.0,
+                       desc="llama-3-8b-shape decode attention, 32768 cached tokens, fp32 KV, batch 16"),
+    "c2-f16-b16": dict(kind="decode", heads=32, kv=8, D=128, n=32768, dtype="f16", B=16, rope=500000.0,
+                       desc="llama-3-8b-shape decode attention, 32768 cached tokens, fp16 KV, batch 16"),
+    "c4-decode": dict(kind="decode", heads=64, kv=8, D=128, n=131072, dtype="f16", B=1, rope=0.0,
+                      desc="llama-3-70b-shape decode attention, 64 q heads / 8 kv heads, 131072 cached fp16 tokens"),
+    "c4-verify": dict(kind="chunk", heads=64, kv=8, D=128, n=131072, dtype="f16", B=1, rope=0.0, nq=8,
+                      q_dtype="f16",
+                      desc="llama-3-70b-shape speculative verify, 8 causal draft queries after 131072 fp16 tokens"),
+    "c3-prefill": dict(kind="chunk", heads=32, kv=8, D=128, n=6144, dtype="bf16", B=1, rope=0.0, nq=2048,
+                       q_dtype="bf16",
+                       desc="llama-3-8b-shape chunked prefill, 2048 causal bf16 queries after 6144 cached tokens"),
+    "c5-mla": dict(kind="mla", heads=128, kv_lora=512, rope_dim=64, n=16384, dtype="bf16", B=1,
+                   desc="MLA absorbed decode, 128 heads, 512+64 latent, 16384 cached bf16 tokens"),
+}
+
+
+def esize(dtype):
+    return 4 if dtype == "f32" else 2
+
+
+def algorithmic(w):
+    """(bytes, flops) per step: K+V payload + Q + O + page table; 4*D flops per (query, key, head)."""
+    if w["kind"] == "mla":
+        width = w["kv_lora"] + w["rope_dim"]
+        pages = math.ceil(w["n"] / 256)
+        b = w["n"] * width * esize(w["dtype"]) + w["heads"] * width * 4 + w["heads"] * w["kv_lora"] * 4 + pages * 4
+        f = 2 * w["heads"] * w["n"] * (width + w["kv_lora"])
+        return b, f
+    nq = w.get("nq", 1)
+    total = w["n"] + (nq if w["kind"] == "chunk" else 0)
+    pages = math.ceil(total / 256)
+    kv_bytes = 2 * total * w["kv"] * w["D"] * esize(w["dtype"])
+    qe = esize(w.get("q_dtype", "f32"))
+    b = w["B"] * (kv_bytes + nq * w["heads"] * w["D"] * (qe + 4) + pages * 4)
+    keys = sum(w["n"] + i + 1 for i in range(nq)) if w["kind"] == "chunk" else w["n"]
+    f = w["B"] * 4 * w["D"] * w["heads"] * keys
+    return b, f
+
+
+def rope_(x, D, pos0, theta):
+    """Rotate-half RoPE in fp32 on rows [n, heads*D], row r at position pos0+r (input synthesis only)."""
+    import torch
+
+    if theta == 0.0:
+        return x
+    n = x.shape[0]
+    half = D // 2
+    inv = torch.pow(torch.tensor(theta, dtype=torch.float64), -2.0 * torch.arange(half, dtype=torch.float64) / D)
+    ang = (torch.arange(n, dtype=torch.float64) + pos0)[:, None] * inv[None, :]
+    c = torch.cos(ang).float().to(x.device)[:, None, :]
+    s = torch.sin(ang).float().to(x.device)[:, None, :]
+    v = x.view(n, -1, D)
+    a, b = v[..., :half].clone(), v[..., half:].clone()
+    v[..., :half] = a * c - b * s
+    v[..., half:] = a * s + b * c
+    return x
+
+
+def to_cache_bits(x, dtype):
+    import torch
+
+    if dtype == "f32":
+        return x.contiguous()
+    t = x.half() if dtype == "f16" else x.bfloat16()
+    return t.contiguous().view(torch.int16)
+
+
+def build_decode(w, gen, dev):
+    """KV handle with R rotation sets of B sequences each, filled on the device."""
+    import torch
+
+    import qauntrunner_amd as qr
+
+    nq = w.get("nq", 1)
+    total = w["n"] + (nq if w["kind"] == "chunk" else 0)
+    set_bytes = w["B"] * 2 * total * w["kv"] * w["D"] * esize(w["dtype"])
+    R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
+    kv = qr.PagedKvCache(1, w["heads"], w["kv"], w["D"], total, kv_dtype=w["dtype"], max_batch=R * w["B"])
+    kv.Reserve(R * w["B"] * math.ceil(total / 256))
+    kv_dim = w["kv"] * w["D"]
+    chunk = 8192
+    for s in range(R * w["B"]):
+        for p0 in range(0, total, chunk):
+            m = min(chunk, total - p0)
+            K = rope_(torch.randn(m, kv_dim, device=dev, generator=gen), w["D"], p0, w["rope"])
+            V = torch.randn(m, kv_dim, device=dev, generator=gen)
+            kv.AppendRangeDev(0, p0, to_cache_bits(K, w["dtype"]), to_cache_bits(V, w["dtype"]),
+                              src_dtype=w["dtype"], seq_id=s)
+    torch.cuda.synchronize()
+    return kv, R
+
+
+def run_gpu(w, steps, warmup):
+    import torch
+
+    import qauntrunner_amd as qr
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    stream = torch.cuda.current_stream()
+
+    if w["kind"] == "mla":
+        width = w["kv_lora"] + w["rope_dim"]
+        set_bytes = w["n"] * width * esize(w["dtype"])
+        R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
+        cache = qr.MlaLatentCache(R, w["kv_lora"], w["rope_dim"], w["n"], dtype=w["dtype"])
+        cache.Reserve(R * math.ceil(w["n"] / 256))
+        for layer in range(R):
+            rows = torch.randn(w["n"], width, device=dev, generator=gen)
+            cache.AppendRangeDev(layer, 0, to_cache_bits(rows, w["dtype"]), src_dtype=w["dtype"])
+        qt = torch.randn(R, w["heads"], w["kv_lora"], device=dev, generator=gen)
+        qrp = torch.randn(R, w["heads"], w["rope_dim"], device=dev, generator=gen)
+        u = torch.empty(R, w["heads"], w["kv_lora"], device=dev)
+        scale = 1.0 / math.sqrt(192.0)
+
+        def step(i):
+            r = i % R
+            cache.AbsorbedAttentionDev(r, w["n"] - 1, qt[r], qrp[r], u[r], scale, stream=stream)
+        handle = cache
+    else:
+        kv, R = build_decode(w, gen, dev)
+        B = w["B"]
+        nq = w.get("nq", 1)
+        row = w["heads"] * w["D"]
+        scale = 1.0 / math.sqrt(w["D"])
+        if w["kind"] == "decode":
+            q = rope_(torch.randn(R * B, row, device=dev, generator=gen), w["D"], w["n"] - 1, w["rope"])
+            out = torch.empty(R * B, row, device=dev)
+
+            def step(i):
+                r = i % R
+                ids = list(range(r * B, (r + 1) * B))
+                kv.AttentionDev(0, ids, [w["n"] - 1] * B, q[r * B:(r + 1) * B], out[r * B:(r + 1) * B], scale,
+                                stream=stream)
+        else:
+            q = to_cache_bits(torch.randn(R, nq, row, device=dev, generator=gen), w["q_dtype"])
+            out = torch.empty(R, nq, row, device=dev)
+
+            def step(i):
+                r = i % R
+                kv.AttentionChunkDev(0, w["n"], q[r], out[r], scale, q_dtype=w["q_dtype"], seq_id=r, stream=stream)
+        handle = kv
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record(stream)
+    for i in range(steps):
+        step(warmup + i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / steps
+    handle.close()
+    return ms, wall * 1e3 / steps
+
+
+def cpu_baseline(w, budget_s=10.0):
+    """Oracle (op-order restatement of the reference's single-threaded path) on one core."""
+    import numpy as np
+
+    from oracle import oracle
+
+    try:
+        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    except (AttributeError, OSError):
+        pass
+    rng = np.random.default_rng(7)
+    bytes_step, _ = algorithmic(w)
+    if w["kind"] == "mla":
+        width = w["kv_lora"] + w["rope_dim"]
+        lat = rng.standard_normal((w["n"], width), dtype=np.float32)
+        qt = rng.standard_normal((w["heads"], w["kv_lora"]), dtype=np.float32)
+        qrp = rng.standard_normal((w["heads"], w["rope_dim"]), dtype=np.float32)
+        heads_sample = 8
+        def call():
+            oracle.mla_attention(lat, qt[:heads_sample], qrp[:heads_sample], w["kv_lora"], w["rope_dim"], 0.072)
+        unit_fraction = heads_sample / w["heads"]
+        sample = f"MLA over {w['n']} tokens for {heads_sample} of {w['heads']} heads, scaled to all heads"
+    else:
+        nq = w.get("nq", 1)
+        total = w["n"] + (nq if w["kind"] == "chunk" else 0)
+        K = rng.standard_normal((total, w["kv"] * w["D"]), dtype=np.float32)
+        V = rng.standard_normal((total, w["kv"] * w["D"]), dtype=np.float32)
+        q = rng.standard_normal(w["heads"] * w["D"], dtype=np.float32)
+        seq = w["n"] + (nq // 2 if w["kind"] == "chunk" else 0)
+        def call():
+            oracle.kv_attention(K[:seq], V[:seq], q, w["heads"], w["kv"], w["D"], 1 / math.sqrt(w["D"]))
+        unit_fraction = 1.0 / (w["B"] * nq)
+        sample = (f"one query over {seq} tokens (a 1/{w['B'] * nq} share of the step), "
+                  "fp32 storage of the same values")
+    times = []
+    start = time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() - start > budget_s or len(times) >= 200:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    step_s = med / unit_fraction
+    return {
+        "value": bytes_step / step_s / 1e12,
+        "unit": "TB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{sample}; median of {len(times)} calls ({med * 1e3:.1f} ms each), "
+                  f"step {step_s * 1e3:.1f} ms",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2-f32-b1", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the kernels are the one-GPU share at its real shape; no multi-GPU path exists)", file=sys.stderr)
+        sys.exit(2)
+
+    w = WORKLOADS[args.config]
+    ms, wall_ms = run_gpu(w, args.steps, args.warmup)
+    bytes_step, flops_step = algorithmic(w)
+    tbs = bytes_step / (ms * 1e-3) / 1e12
+    nq = w.get("nq", 1)
+    tokens = w["B"] * nq
+    dtype = w["dtype"]
+    mfma = w["kind"] == "chunk" and nq > 64
+    if mfma:
+        achieved = flops_step / (ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": MFMA_PEAK_TFS.get(dtype, 2500.0),
+                "unit": "TFLOP/s", "frac": achieved / MFMA_PEAK_TFS.get(dtype, 2500.0), "traffic": None}
+    else:
+        roof = {"bound": "hbm", "achieved": tbs * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
+                "frac": tbs / HBM_PEAK_TBS, "traffic": None}
+    line = {
+        "metric": METRIC,
+        "value": round(tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "us_per_token": round(ms * 1e3 / tokens, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic N(0,1) on device" + (", RoPE base 500000 on Q/K" if w.get("rope") else ""),
+        "config": {"workload": w["desc"], "name": args.config, "algorithmic_bytes": bytes_step,
+                   "algorithmic_flops": flops_step, "host_wall_ms_per_step": round(wall_ms, 4)},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

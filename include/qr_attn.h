@@ -1,0 +1,177 @@
+/*
+ * qr_attn.h -- C ABI of the MI355X (gfx950) paged-KV attention library.
+ *
+ * This is the drop-in boundary for QuantRunner's attention path.  The C#
+ * classes PagedKvCache and MlaLatentCache keep their public members and
+ * forward here through P/Invoke; every entry point below names the reference
+ * member it replaces (paths relative to src/QuantRunner.Core).
+ *
+ * Conventions
+ *  - Every call returns an int status: QR_OK (0) or a negative QR_ERR_* code.
+ *    qr_last_error() returns a thread-local message for the last failure.
+ *    Invalid arguments are reported, never dereferenced.
+ *  - Handles are not thread-safe (the reference classes are not either);
+ *    callers serialise calls on one handle.
+ *  - Host-pointer calls are synchronous: on return the output is written and
+ *    the inputs may be reused, like the reference's blocking methods.
+ *  - *_dev calls take device pointers and a hipStream_t (passed as void*,
+ *    NULL = the null stream) and return without synchronising.
+ *  - A page holds QR_PAGE_TOKENS tokens.  Pages are allocated on first
+ *    append of any of their positions and are zero-filled when allocated.
+ *    Reset/Truncate keep pages (PagedKvCache.cs:72-76).
+ *  - 16-bit data crosses the boundary as raw IEEE bit patterns (uint16_t).
+ *    float -> fp16 conversion follows Dtypes.FloatToF16 (Dtypes.cs:100-126:
+ *    ties away from zero in the normal range), float -> bf16 follows
+ *    Dtypes.FloatToBf16 (round to nearest even, :132-139); 16-bit -> float
+ *    is exact.
+ */
+#ifndef QR_ATTN_H
+#define QR_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QR_ATTN_ABI_VERSION 1
+#define QR_PAGE_TOKENS 256 /* PagedKvCache.PageTokens, PagedKvCache.cs:14 */
+
+/* element types of caches and inputs */
+enum {
+    QR_DTYPE_F32 = 0,
+    QR_DTYPE_F16 = 1,
+    QR_DTYPE_BF16 = 2
+};
+
+/* status codes */
+enum {
+    QR_OK = 0,
+    QR_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad shape, dtype, layer or sequence id   */
+    QR_ERR_OUT_OF_RANGE = -2,     /* pos >= max_seq, or a row longer than kv_dim           */
+    QR_ERR_OUT_OF_MEMORY = -3,    /* device or host allocation failed                      */
+    QR_ERR_HIP = -4,              /* a HIP runtime call failed (message has the HIP error) */
+    QR_ERR_NOT_RESIDENT = -5      /* attention over a position whose page was never appended */
+};
+
+typedef struct qr_kv qr_kv;   /* PagedKvCache  */
+typedef struct qr_mla qr_mla; /* MlaLatentCache */
+
+/* ---- library ---------------------------------------------------------- */
+int qr_abi_version(void);
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* qr_last_error(void);
+/* Static name of a status code, e.g. "QR_ERR_OUT_OF_RANGE". */
+const char* qr_status_name(int status);
+
+/* ---- PagedKvCache ------------------------------------------------------ */
+
+/* ctor PagedKvCache(layers, heads, kvHeads, headDim, maxSeq), PagedKvCache.cs:29-37.
+ * kv_dtype: QR_DTYPE_F32 (the reference's page type, PagedKvCache.cs:17-18),
+ * F16 or BF16.  max_batch: number of independent sequences (seq_id 0..max_batch-1),
+ * each with its own page table; 1 reproduces the reference.  head_dim must be
+ * one of 16, 32, 64, 128, 256. */
+int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim, int max_seq,
+                 int kv_dtype, int max_batch);
+int qr_kv_destroy(qr_kv* kv);
+
+/* Pre-sizes the device page pool to hold at least `pages` pages so that later
+ * appends do not grow it.  No reference counterpart (the reference allocates
+ * per page from the managed heap). */
+int qr_kv_reserve(qr_kv* kv, int pages);
+
+/* Append(layer, pos, k, v), PagedKvCache.cs:62-69.  k/v are host fp32 rows of
+ * k_len/v_len floats.  A row longer than kv_dim is an error (the reference's
+ * Span.CopyTo throws); a shorter one overwrites only its first elements, as
+ * Span.CopyTo does.  SeqLen(seq) = max(SeqLen, pos+1). */
+int qr_kv_append(qr_kv* kv, int seq_id, int layer, int pos, const float* k, int k_len,
+                 const float* v, int v_len);
+
+/* Bulk Append of n consecutive positions pos0..pos0+n-1: k/v are host rows
+ * [n][kv_dim] of src_dtype, converted to the cache dtype.  Equivalent to n
+ * Append calls. */
+int qr_kv_append_range(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k,
+                       const void* v, int src_dtype);
+/* Same with device-resident rows, enqueued on `stream`. */
+int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k_dev,
+                           const void* v_dev, int src_dtype, void* stream);
+
+/* Attention(layer, pos, q, attn, scale), PagedKvCache.cs:83-136:
+ * attn[h*D:(h+1)*D] = softmax(q_h . K[0..pos, kvh(h)] * scale) . V[0..pos, kvh(h)],
+ * kvh(h) = h*kv_heads/heads.  q and attn are host fp32 [heads*head_dim]. */
+int qr_kv_attention(qr_kv* kv, int seq_id, int layer, int pos, const float* q, float* attn,
+                    float scale);
+
+/* n independent decode queries, entry i over sequence seq_ids[i] at position
+ * pos[i]; q/attn are host fp32 [n][heads*head_dim].  Equivalent to n
+ * qr_kv_attention calls. */
+int qr_kv_attention_batch(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
+                          const float* q, float* attn, float scale);
+/* Same with device q/attn, enqueued on `stream`.  seq_ids/pos stay host arrays. */
+int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
+                        const float* q_dev, float* attn_dev, float scale, void* stream);
+
+/* Causal multi-query attention over one sequence: query i sits at position
+ * pos0+i and attends positions 0..pos0+i.  This is what nq sequential
+ * Attention calls with interleaved appends compute (chunked prompt
+ * processing, StreamingEngine.cs:831-836; speculative verify,
+ * SpeculativeRunner.cs:85-93).  Positions pos0..pos0+nq-1 must already be
+ * appended.  q: host [nq][heads*head_dim] in q_dtype; attn: host fp32. */
+int qr_kv_attention_chunk(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void* q,
+                          int q_dtype, float* attn, float scale);
+int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq,
+                              const void* q_dev, int q_dtype, float* attn_dev, float scale,
+                              void* stream);
+
+/* Reset(), PagedKvCache.cs:72 (seq_id < 0 resets every sequence). */
+int qr_kv_reset(qr_kv* kv, int seq_id);
+/* Truncate(len), PagedKvCache.cs:76: SeqLen = min(SeqLen, len). */
+int qr_kv_truncate(qr_kv* kv, int seq_id, int len);
+/* SeqLen, PagedKvCache.cs:26. */
+int qr_kv_seq_len(const qr_kv* kv, int seq_id, int* out);
+/* BytesUsed, PagedKvCache.cs:27,56: pages x 256 x kv_dim x elem_bytes x 2 summed over
+ * layers and sequences (elem_bytes 4 for f32, matching the reference; 2 for 16-bit). */
+int qr_kv_bytes_used(const qr_kv* kv, long long* out);
+/* BytesPerToken, PagedKvCache.cs:39: kv_dim x elem_bytes x 2 x layers. */
+int qr_kv_bytes_per_token(const qr_kv* kv, long long* out);
+/* Copies rows pos0..pos0+n-1 of one layer back to the host as cache-dtype
+ * rows [n][kv_dim] (debug copy-out; positions must be resident). */
+int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, void* v_out);
+
+/* ---- MlaLatentCache ---------------------------------------------------- */
+
+/* ctor MlaLatentCache(layers, latentDim, maxSeq), MlaLatentCache.cs:22-27, with
+ * latentDim = kv_lora + rope (StreamingEngine.cs:96).  dtype: F32, F16 or BF16.
+ * kv_lora must be a multiple of 64 (<= 1024) and rope a multiple of 16 (<= 256). */
+int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, int dtype);
+int qr_mla_destroy(qr_mla* mla);
+int qr_mla_reserve(qr_mla* mla, int pages);
+/* Append(layer, pos, latent), MlaLatentCache.cs:45-51 (row of `len` floats <= latentDim). */
+int qr_mla_append(qr_mla* mla, int layer, int pos, const float* latent, int len);
+/* Bulk Append of rows [n][latentDim] in src_dtype. */
+int qr_mla_append_range(qr_mla* mla, int layer, int pos0, int n, const void* rows, int src_dtype);
+int qr_mla_append_range_dev(qr_mla* mla, int layer, int pos0, int n, const void* rows_dev,
+                            int src_dtype, void* stream);
+/* Absorbed attention against the latent cache, StreamingEngine.cs:531-568:
+ *   s_t = (q_tilde_h . c_t[0:kv_lora] + q_rope_h . c_t[kv_lora:]) * scale
+ *   u_h = sum_t softmax(s)_t * c_t[0:kv_lora]
+ * for t = 0..pos.  q_tilde [heads][kv_lora], q_rope [heads][rope], u [heads][kv_lora],
+ * all host fp32.  The q-absorb (:517-529) and W_UV (:569-576) projections stay
+ * with the caller. */
+int qr_mla_attention(qr_mla* mla, int layer, int pos, int heads, const float* q_tilde,
+                     const float* q_rope, float scale, float* u);
+int qr_mla_attention_dev(qr_mla* mla, int layer, int pos, int heads, const float* q_tilde_dev,
+                         const float* q_rope_dev, float scale, float* u_dev, void* stream);
+int qr_mla_reset(qr_mla* mla);                    /* MlaLatentCache.cs:53 */
+int qr_mla_truncate(qr_mla* mla, int len);        /* MlaLatentCache.cs:57 */
+int qr_mla_seq_len(const qr_mla* mla, int* out);  /* MlaLatentCache.cs:19 */
+int qr_mla_bytes_used(const qr_mla* mla, long long* out); /* MlaLatentCache.cs:20,40 */
+int qr_mla_page_count(const qr_mla* mla, int layer, int* out); /* MlaLatentCache.cs:60 */
+/* Page(layer, page), MlaLatentCache.cs:63: copies one page out as fp32
+ * [256][latentDim] (16-bit caches decoded exactly). */
+int qr_mla_read_page(qr_mla* mla, int layer, int page, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QR_ATTN_H */

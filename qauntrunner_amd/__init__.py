@@ -1,0 +1,27 @@
+"""qauntrunner_amd -- MI355X (gfx950) paged-KV attention for QuantRunner.
+
+The product is the C-ABI library ``libqr_attn.so`` (include/qr_attn.h) built
+from ``csrc/``; this package holds its ctypes binding and the host-side
+mirror of the reference classes PagedKvCache and MlaLatentCache.
+"""
+from ._lib import (
+    DTYPE_BF16,
+    DTYPE_F16,
+    DTYPE_F32,
+    LIB_PATH,
+    PAGE_TOKENS,
+    QrError,
+    QrHipError,
+    QrInvalidArgument,
+    QrNotResident,
+    QrOutOfMemory,
+    QrOutOfRange,
+    load,
+)
+from .caches import MlaLatentCache, PagedKvCache, dtype_code
+
+__all__ = [
+    "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "LIB_PATH", "PAGE_TOKENS",
+    "QrError", "QrHipError", "QrInvalidArgument", "QrNotResident", "QrOutOfMemory", "QrOutOfRange",
+    "load", "MlaLatentCache", "PagedKvCache", "dtype_code",
+]

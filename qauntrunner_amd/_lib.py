@@ -1,0 +1,128 @@
+"""ctypes binding of libqr_attn.so (the C ABI declared in include/qr_attn.h).
+
+The shared library is built in-tree by ``__graft_entry__.build()`` (hipcc,
+gfx950).  There is no fallback: if the library is missing or cannot be
+loaded, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqr_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qr_attn.h")
+
+PAGE_TOKENS = 256
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+DTYPES = {"f32": DTYPE_F32, "f16": DTYPE_F16, "bf16": DTYPE_BF16}
+
+QR_OK = 0
+QR_ERR_INVALID_ARGUMENT = -1
+QR_ERR_OUT_OF_RANGE = -2
+QR_ERR_OUT_OF_MEMORY = -3
+QR_ERR_HIP = -4
+QR_ERR_NOT_RESIDENT = -5
+
+
+class QrError(Exception):
+    """Base class of every error reported by libqr_attn."""
+
+    status = None
+
+
+class QrInvalidArgument(QrError, ValueError):
+    status = QR_ERR_INVALID_ARGUMENT
+
+
+class QrOutOfRange(QrError, IndexError):
+    status = QR_ERR_OUT_OF_RANGE
+
+
+class QrOutOfMemory(QrError, MemoryError):
+    status = QR_ERR_OUT_OF_MEMORY
+
+
+class QrHipError(QrError, RuntimeError):
+    status = QR_ERR_HIP
+
+
+class QrNotResident(QrError, LookupError):
+    status = QR_ERR_NOT_RESIDENT
+
+
+_ERRORS = {c.status: c for c in (QrInvalidArgument, QrOutOfRange, QrOutOfMemory, QrHipError, QrNotResident)}
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_ip = ctypes.POINTER(ctypes.c_int)
+_llp = ctypes.POINTER(ctypes.c_longlong)
+_pp = ctypes.POINTER(ctypes.c_void_p)
+
+# name -> argtypes (every function returns int unless listed in _RESTYPES)
+SIGNATURES = {
+    "qr_abi_version": [],
+    "qr_last_error": [],
+    "qr_status_name": [_i],
+    "qr_kv_create": [_pp, _i, _i, _i, _i, _i, _i, _i],
+    "qr_kv_destroy": [_p],
+    "qr_kv_reserve": [_p, _i],
+    "qr_kv_append": [_p, _i, _i, _i, _p, _i, _p, _i],
+    "qr_kv_append_range": [_p, _i, _i, _i, _i, _p, _p, _i],
+    "qr_kv_append_range_dev": [_p, _i, _i, _i, _i, _p, _p, _i, _p],
+    "qr_kv_attention": [_p, _i, _i, _i, _p, _p, _f],
+    "qr_kv_attention_batch": [_p, _i, _p, _i, _p, _p, _p, _f],
+    "qr_kv_attention_dev": [_p, _i, _p, _i, _p, _p, _p, _f, _p],
+    "qr_kv_attention_chunk": [_p, _i, _i, _i, _i, _p, _i, _p, _f],
+    "qr_kv_attention_chunk_dev": [_p, _i, _i, _i, _i, _p, _i, _p, _f, _p],
+    "qr_kv_reset": [_p, _i],
+    "qr_kv_truncate": [_p, _i, _i],
+    "qr_kv_seq_len": [_p, _i, _ip],
+    "qr_kv_bytes_used": [_p, _llp],
+    "qr_kv_bytes_per_token": [_p, _llp],
+    "qr_kv_read": [_p, _i, _i, _i, _i, _p, _p],
+    "qr_mla_create": [_pp, _i, _i, _i, _i, _i],
+    "qr_mla_destroy": [_p],
+    "qr_mla_reserve": [_p, _i],
+    "qr_mla_append": [_p, _i, _i, _p, _i],
+    "qr_mla_append_range": [_p, _i, _i, _i, _p, _i],
+    "qr_mla_append_range_dev": [_p, _i, _i, _i, _p, _i, _p],
+    "qr_mla_attention": [_p, _i, _i, _i, _p, _p, _f, _p],
+    "qr_mla_attention_dev": [_p, _i, _i, _i, _p, _p, _f, _p, _p],
+    "qr_mla_reset": [_p],
+    "qr_mla_truncate": [_p, _i],
+    "qr_mla_seq_len": [_p, _ip],
+    "qr_mla_bytes_used": [_p, _llp],
+    "qr_mla_page_count": [_p, _i, _ip],
+    "qr_mla_read_page": [_p, _i, _i, _p],
+}
+_RESTYPES = {"qr_last_error": ctypes.c_char_p, "qr_status_name": ctypes.c_char_p}
+
+_lib = None
+
+
+def load():
+    """Loads libqr_attn.so once; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raises the QrError subclass of a non-zero status with the library's message."""
+    if status == QR_OK:
+        return
+    lib = load()
+    msg = lib.qr_last_error().decode(errors="replace")
+    name = lib.qr_status_name(status).decode()
+    raise _ERRORS.get(status, QrError)(f"{name}: {msg}")

@@ -1,0 +1,287 @@
+"""Host-side mirror of QuantRunner's attention caches over libqr_attn.
+
+``PagedKvCache`` and ``MlaLatentCache`` keep the member names and argument
+meaning of the C# classes (src/QuantRunner.Core/Runtime/PagedKvCache.cs,
+MlaLatentCache.cs) and forward every call to the C ABI.  Host-array calls
+take numpy arrays (fp32, or uint16 bit patterns for 16-bit data) and are
+synchronous; the ``*Dev`` calls take torch tensors already on the GPU and
+enqueue on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import DTYPES, PAGE_TOKENS, check
+
+__all__ = ["PagedKvCache", "MlaLatentCache", "dtype_code"]
+
+
+def dtype_code(dt) -> int:
+    if isinstance(dt, int):
+        return dt
+    return DTYPES[dt]
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _host_rows(x, src_dtype: int):
+    """Contiguous host rows: fp32 for DTYPE_F32, uint16 bit patterns otherwise."""
+    want = np.float32 if src_dtype == _lib.DTYPE_F32 else np.uint16
+    a = np.ascontiguousarray(x)
+    if a.dtype != want:
+        raise TypeError(f"expected {np.dtype(want).name} rows for dtype code {src_dtype}, got {a.dtype}")
+    return a
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(getattr(stream, "cuda_stream", stream))
+
+
+class PagedKvCache:
+    """Paged K/V store with fused GQA decode attention (PagedKvCache.cs:12-136)."""
+
+    PageTokens = PAGE_TOKENS  # PagedKvCache.cs:14
+
+    def __init__(self, layers, heads, kv_heads, head_dim, max_seq, kv_dtype="f32", max_batch=1):
+        self._lib = _lib.load()
+        h = ctypes.c_void_p()
+        check(self._lib.qr_kv_create(ctypes.byref(h), layers, heads, kv_heads, head_dim, max_seq,
+                                     dtype_code(kv_dtype), max_batch))
+        self._h = h
+        self.Layers, self.Heads, self.KvHeads, self.HeadDim = layers, heads, kv_heads, head_dim
+        self.MaxSeq, self.MaxBatch = max_seq, max_batch
+        self.KvDtype = dtype_code(kv_dtype)
+        self.KvDim = kv_heads * head_dim
+
+    # ---- lifetime
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            check(self._lib.qr_kv_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- properties
+    def seq_len(self, seq_id=0) -> int:
+        out = ctypes.c_int()
+        check(self._lib.qr_kv_seq_len(self._h, seq_id, ctypes.byref(out)))
+        return out.value
+
+    @property
+    def SeqLen(self) -> int:  # PagedKvCache.cs:26
+        return self.seq_len(0)
+
+    @property
+    def BytesUsed(self) -> int:  # PagedKvCache.cs:27
+        out = ctypes.c_longlong()
+        check(self._lib.qr_kv_bytes_used(self._h, ctypes.byref(out)))
+        return out.value
+
+    @property
+    def BytesPerToken(self) -> int:  # PagedKvCache.cs:39
+        out = ctypes.c_longlong()
+        check(self._lib.qr_kv_bytes_per_token(self._h, ctypes.byref(out)))
+        return out.value
+
+    def Reserve(self, pages: int) -> None:
+        check(self._lib.qr_kv_reserve(self._h, pages))
+
+    # ---- writes
+    def Append(self, layer, pos, k, v, seq_id=0) -> None:
+        """PagedKvCache.Append (:62-69): fp32 rows of at most kv_dim floats."""
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        check(self._lib.qr_kv_append(self._h, seq_id, layer, pos, _ptr(k), k.size, _ptr(v), v.size))
+
+    def AppendRange(self, layer, pos0, k_rows, v_rows, src_dtype="f32", seq_id=0) -> None:
+        code = dtype_code(src_dtype)
+        k = _host_rows(k_rows, code)
+        v = _host_rows(v_rows, code)
+        n = k.size // self.KvDim
+        if k.size != n * self.KvDim or v.size != k.size:
+            raise ValueError("k/v rows must both be [n, kv_dim]")
+        check(self._lib.qr_kv_append_range(self._h, seq_id, layer, pos0, n, _ptr(k), _ptr(v), code))
+
+    def AppendRangeDev(self, layer, pos0, k_rows, v_rows, src_dtype="f32", seq_id=0, stream=None) -> None:
+        n = k_rows.numel() // self.KvDim
+        check(self._lib.qr_kv_append_range_dev(self._h, seq_id, layer, pos0, n, ctypes.c_void_p(k_rows.data_ptr()),
+                                               ctypes.c_void_p(v_rows.data_ptr()), dtype_code(src_dtype),
+                                               _stream_ptr(stream)))
+
+    def Reset(self, seq_id=-1) -> None:  # PagedKvCache.cs:72
+        check(self._lib.qr_kv_reset(self._h, seq_id))
+
+    def Truncate(self, length, seq_id=0) -> None:  # PagedKvCache.cs:76
+        check(self._lib.qr_kv_truncate(self._h, seq_id, length))
+
+    # ---- attention
+    def Attention(self, layer, pos, q, scale, seq_id=0) -> np.ndarray:
+        """PagedKvCache.Attention (:83-136); returns attn [heads*head_dim] fp32."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        if q.size != self.Heads * self.HeadDim:
+            raise ValueError(f"q must hold heads*head_dim = {self.Heads * self.HeadDim} floats")
+        out = np.empty(self.Heads * self.HeadDim, np.float32)
+        check(self._lib.qr_kv_attention(self._h, seq_id, layer, pos, _ptr(q), _ptr(out), scale))
+        return out
+
+    def AttentionBatch(self, layer, seq_ids, positions, q, scale) -> np.ndarray:
+        ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        n = ids.size
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        if pos.size != n or q.size != n * self.Heads * self.HeadDim:
+            raise ValueError("seq_ids, positions and q rows must agree")
+        out = np.empty((n, self.Heads * self.HeadDim), np.float32)
+        check(self._lib.qr_kv_attention_batch(self._h, n, _ptr(ids), layer, _ptr(pos), _ptr(q), _ptr(out), scale))
+        return out
+
+    def AttentionDev(self, layer, seq_ids, positions, q, out, scale, stream=None) -> None:
+        ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        check(self._lib.qr_kv_attention_dev(self._h, ids.size, _ptr(ids), layer, _ptr(pos),
+                                            ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                            scale, _stream_ptr(stream)))
+
+    def AttentionChunk(self, layer, pos0, q, scale, q_dtype="f32", seq_id=0) -> np.ndarray:
+        """Causal attention of nq queries at pos0..pos0+nq-1 (each sees 0..its position)."""
+        code = dtype_code(q_dtype)
+        q = _host_rows(q, code)
+        row = self.Heads * self.HeadDim
+        nq = q.size // row
+        if q.size != nq * row:
+            raise ValueError("q must be [nq, heads*head_dim]")
+        out = np.empty((nq, row), np.float32)
+        check(self._lib.qr_kv_attention_chunk(self._h, seq_id, layer, pos0, nq, _ptr(q), code, _ptr(out), scale))
+        return out
+
+    def AttentionChunkDev(self, layer, pos0, q, out, scale, q_dtype="f32", seq_id=0, stream=None) -> None:
+        nq = q.numel() // (self.Heads * self.HeadDim)
+        check(self._lib.qr_kv_attention_chunk_dev(self._h, seq_id, layer, pos0, nq, ctypes.c_void_p(q.data_ptr()),
+                                                  dtype_code(q_dtype), ctypes.c_void_p(out.data_ptr()), scale,
+                                                  _stream_ptr(stream)))
+
+    # ---- debug copy-out
+    def Read(self, layer, pos0, n, seq_id=0):
+        """Rows pos0..pos0+n-1 as stored (fp32, or uint16 bits for 16-bit caches)."""
+        dt = np.float32 if self.KvDtype == _lib.DTYPE_F32 else np.uint16
+        k = np.empty((n, self.KvDim), dt)
+        v = np.empty((n, self.KvDim), dt)
+        check(self._lib.qr_kv_read(self._h, seq_id, layer, pos0, n, _ptr(k), _ptr(v)))
+        return k, v
+
+
+class MlaLatentCache:
+    """Paged MLA latent store with absorbed attention (MlaLatentCache.cs:10-65,
+    StreamingEngine.cs:531-568)."""
+
+    PageTokens = PAGE_TOKENS
+
+    def __init__(self, layers, kv_lora, rope, max_seq, dtype="f32"):
+        self._lib = _lib.load()
+        h = ctypes.c_void_p()
+        check(self._lib.qr_mla_create(ctypes.byref(h), layers, kv_lora, rope, max_seq, dtype_code(dtype)))
+        self._h = h
+        self.Layers, self.KvLora, self.Rope, self.MaxSeq = layers, kv_lora, rope, max_seq
+        self.LatentDim = kv_lora + rope
+        self.Dtype = dtype_code(dtype)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            check(self._lib.qr_mla_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def SeqLen(self) -> int:
+        out = ctypes.c_int()
+        check(self._lib.qr_mla_seq_len(self._h, ctypes.byref(out)))
+        return out.value
+
+    @property
+    def BytesUsed(self) -> int:
+        out = ctypes.c_longlong()
+        check(self._lib.qr_mla_bytes_used(self._h, ctypes.byref(out)))
+        return out.value
+
+    def PageCount(self, layer) -> int:
+        out = ctypes.c_int()
+        check(self._lib.qr_mla_page_count(self._h, layer, ctypes.byref(out)))
+        return out.value
+
+    def Page(self, layer, page) -> np.ndarray:
+        out = np.empty((PAGE_TOKENS, self.LatentDim), np.float32)
+        check(self._lib.qr_mla_read_page(self._h, layer, page, _ptr(out)))
+        return out
+
+    def Reserve(self, pages: int) -> None:
+        check(self._lib.qr_mla_reserve(self._h, pages))
+
+    def Append(self, layer, pos, latent) -> None:
+        row = np.ascontiguousarray(latent, dtype=np.float32).reshape(-1)
+        check(self._lib.qr_mla_append(self._h, layer, pos, _ptr(row), row.size))
+
+    def AppendRange(self, layer, pos0, rows, src_dtype="f32") -> None:
+        code = dtype_code(src_dtype)
+        r = _host_rows(rows, code)
+        n = r.size // self.LatentDim
+        if r.size != n * self.LatentDim:
+            raise ValueError("rows must be [n, kv_lora + rope]")
+        check(self._lib.qr_mla_append_range(self._h, layer, pos0, n, _ptr(r), code))
+
+    def AppendRangeDev(self, layer, pos0, rows, src_dtype="f32", stream=None) -> None:
+        n = rows.numel() // self.LatentDim
+        check(self._lib.qr_mla_append_range_dev(self._h, layer, pos0, n, ctypes.c_void_p(rows.data_ptr()),
+                                                dtype_code(src_dtype), _stream_ptr(stream)))
+
+    def Reset(self) -> None:
+        check(self._lib.qr_mla_reset(self._h))
+
+    def Truncate(self, length) -> None:
+        check(self._lib.qr_mla_truncate(self._h, length))
+
+    def AbsorbedAttention(self, layer, pos, q_tilde, q_rope, scale) -> np.ndarray:
+        """u [heads, kv_lora] = softmax(q~.c + q_rope.k_pe) . c over positions 0..pos."""
+        qt = np.ascontiguousarray(q_tilde, dtype=np.float32)
+        heads = qt.size // self.KvLora
+        qr = np.ascontiguousarray(q_rope if self.Rope else np.zeros(1), dtype=np.float32)
+        if self.Rope and qr.size != heads * self.Rope:
+            raise ValueError("q_rope must be [heads, rope]")
+        u = np.empty((heads, self.KvLora), np.float32)
+        check(self._lib.qr_mla_attention(self._h, layer, pos, heads, _ptr(qt), _ptr(qr), scale, _ptr(u)))
+        return u
+
+    def AbsorbedAttentionDev(self, layer, pos, q_tilde, q_rope, u, scale, stream=None) -> None:
+        heads = q_tilde.numel() // self.KvLora
+        qr_ptr = ctypes.c_void_p(q_rope.data_ptr()) if q_rope is not None else ctypes.c_void_p()
+        check(self._lib.qr_mla_attention_dev(self._h, layer, pos, heads, ctypes.c_void_p(q_tilde.data_ptr()),
+                                             qr_ptr, scale, ctypes.c_void_p(u.data_ptr()), _stream_ptr(stream)))

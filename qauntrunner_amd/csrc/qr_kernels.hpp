@@ -1,0 +1,86 @@
+// qr_kernels.hpp -- launch interfaces shared by the translation units of libqr_attn.
+#pragma once
+
+#include "qr_common.hpp"
+
+namespace qr {
+
+// ------------------------------------------------------------------ paging
+// Page layout in the HBM pool (elements of the cache dtype):
+//   page = planes x kv_heads x kPageTokens x head_dim
+// plane 0 holds K, plane 1 holds V (GQA cache); the MLA cache has one plane with
+// kv_heads = 1 and head_dim = latent width.  Inside a plane each kv head owns a
+// contiguous [kPageTokens][head_dim] block, so one (page, kv head) is a single
+// contiguous stream of 256 rows.
+struct PageGeom {
+    int planes;
+    int kv_heads;
+    int head_dim;
+    __host__ __device__ long long plane_elems() const { return (long long)kv_heads * kPageTokens * head_dim; }
+    __host__ __device__ long long page_elems() const { return plane_elems() * planes; }
+};
+
+// Writes rows pos0..pos0+n-1 of `planes` source arrays into their pages.
+// src[p] is [n][src_stride] of src_dtype; only the first row_len[p] elements of
+// each row are written (row_len <= kv_heads*head_dim).
+struct AppendArgs {
+    void* pool;
+    const int* page_table;  // device, entries of this (sequence, layer)
+    PageGeom geom;
+    int dtype;              // cache dtype
+    const void* src[2];
+    int row_len[2];
+    int src_stride;
+    int src_dtype;
+    int pos0;
+    int n;
+};
+hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
+
+// Gathers rows back out in the cache dtype ([n][kv_heads*head_dim] per plane),
+// or decoded to fp32 when to_f32 is set.
+struct GatherArgs {
+    const void* pool;
+    const int* page_table;
+    PageGeom geom;
+    int dtype;
+    void* dst[2];
+    int pos0;
+    int n;
+    int to_f32;
+};
+hipError_t launch_gather(const GatherArgs& a, hipStream_t stream);
+
+// Widens 16-bit rows to fp32 (exact) -- used for 16-bit query inputs.
+hipError_t launch_widen(const void* src, int src_dtype, float* dst, long long n, hipStream_t stream);
+
+// ------------------------------------------------------------------ GQA decode
+constexpr int kMaxDecodeBatch = 64;  // decode entries per launch (descriptor passed by value)
+
+struct DecodeArgs {
+    const void* pool;
+    const int* page_table;  // device page table (all sequences and layers)
+    PageGeom geom;          // planes = 2
+    int dtype;              // cache dtype
+    int heads;
+    const float* q;         // [nb][heads*head_dim]
+    float* out;             // [nb][heads*head_dim]
+    float scale;
+    int nb;
+    int seq_len[kMaxDecodeBatch];  // positions attended per entry (pos + 1)
+    int pt_off[kMaxDecodeBatch];   // offset of the entry's page-table row
+};
+
+// Split-K plan for one launch.
+struct DecodePlan {
+    int split_tokens;  // tokens per workgroup
+    int max_splits;    // splits of the longest entry
+    int units;         // workgroups per (entry, split): kv heads x head chunks, or heads
+    size_t workspace_bytes;
+};
+DecodePlan plan_decode(const DecodeArgs& a);
+// workspace: at least plan.workspace_bytes of device memory.
+hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, void* workspace,
+                         hipStream_t stream);
+
+}  // namespace qr

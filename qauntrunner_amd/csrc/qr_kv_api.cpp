@@ -1,0 +1,441 @@
+// qr_kv.cpp -- C ABI of the paged GQA KV cache (PagedKvCache, PagedKvCache.cs:12-136).
+#include <algorithm>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "qr_store.hpp"
+
+namespace qr {
+const char* last_error();
+}
+
+using namespace qr;
+
+struct qr_kv {
+    int device = 0;
+    int layers = 0, heads = 0, kv_heads = 0, head_dim = 0, max_seq = 0, dtype = 0, max_batch = 0;
+    int kv_dim = 0;
+    PagedStore store;
+    std::vector<int> seq_len;
+    hipStream_t stream = nullptr;
+    DevBuf stage;      // host <-> device staging of rows, queries and outputs
+    DevBuf workspace;  // split-K partials
+};
+
+namespace {
+
+int check_handle(const qr_kv* kv) {
+    if (!kv) {
+        set_error("null qr_kv handle");
+        return QR_ERR_INVALID_ARGUMENT;
+    }
+    return QR_OK;
+}
+
+int check_seq_layer(const qr_kv* kv, int seq_id, int layer) {
+    QR_CHECK_ARG(seq_id >= 0 && seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
+    QR_CHECK_ARG(layer >= 0 && layer < kv->layers, "layer %d outside [0, %d)", layer, kv->layers);
+    return QR_OK;
+}
+
+int check_pos(const qr_kv* kv, int pos) {
+    if (pos < 0 || pos >= kv->max_seq) {
+        set_error("position %d outside [0, max_seq=%d)", pos, kv->max_seq);
+        return QR_ERR_OUT_OF_RANGE;
+    }
+    return QR_OK;
+}
+
+int check_resident(const qr_kv* kv, int seq_id, int layer, int pos) {
+    if (!kv->store.resident(seq_id, layer, pos)) {
+        set_error("position %d of sequence %d layer %d was never appended (%d pages resident)", pos,
+                  seq_id, layer, kv->store.pages_held(seq_id, layer));
+        return QR_ERR_NOT_RESIDENT;
+    }
+    return QR_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Appends rows already on the device (src_dtype, row stride kv_dim).
+int append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k, const void* v,
+               int k_len, int v_len, int src_dtype, hipStream_t stream) {
+    QR_TRY(kv->store.ensure(seq_id, layer, pos0 + n, stream));
+    AppendArgs a{};
+    a.pool = kv->store.pool();
+    a.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+    a.geom = kv->store.geom();
+    a.dtype = kv->dtype;
+    a.src[0] = k;
+    a.src[1] = v;
+    a.row_len[0] = k_len;
+    a.row_len[1] = v_len;
+    a.src_stride = kv->kv_dim;
+    a.src_dtype = src_dtype;
+    a.pos0 = pos0;
+    a.n = n;
+    QR_HIP(launch_append(a, stream));
+    int& sl = kv->seq_len[seq_id];
+    sl = std::max(sl, pos0 + n);  // PagedKvCache.cs:68
+    return QR_OK;
+}
+
+// Runs decode entries (seq_ids[i], seq_len[i]) with device q/out rows.
+int decode_dev(qr_kv* kv, int n, const int* seq_ids, const int* seq_len, int layer, const float* q,
+               float* out, float scale, hipStream_t stream) {
+    const size_t row = static_cast<size_t>(kv->heads) * kv->head_dim;
+    for (int i0 = 0; i0 < n; i0 += kMaxDecodeBatch) {
+        const int nb = std::min(kMaxDecodeBatch, n - i0);
+        DecodeArgs a{};
+        a.pool = kv->store.pool();
+        a.page_table = kv->store.page_table_dev();
+        a.geom = kv->store.geom();
+        a.dtype = kv->dtype;
+        a.heads = kv->heads;
+        a.q = q + i0 * row;
+        a.out = out + i0 * row;
+        a.scale = scale;
+        a.nb = nb;
+        for (int i = 0; i < nb; ++i) {
+            a.seq_len[i] = seq_len[i0 + i];
+            a.pt_off[i] = kv->store.pt_offset(seq_ids[i0 + i], layer);
+        }
+        const DecodePlan plan = plan_decode(a);
+        QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+        QR_HIP(launch_decode(a, plan, kv->workspace.get(), stream));
+    }
+    return QR_OK;
+}
+
+int validate_batch(const qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
+                   std::vector<int>& seq_len) {
+    QR_CHECK_ARG(n >= 1, "batch size must be >= 1 (got %d)", n);
+    QR_CHECK_ARG(seq_ids && pos, "null seq_ids/pos array");
+    seq_len.resize(n);
+    for (int i = 0; i < n; ++i) {
+        QR_TRY(check_seq_layer(kv, seq_ids[i], layer));
+        QR_TRY(check_pos(kv, pos[i]));
+        QR_TRY(check_resident(kv, seq_ids[i], layer, pos[i]));
+        seq_len[i] = pos[i] + 1;
+    }
+    return QR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_abi_version(void) { return QR_ATTN_ABI_VERSION; }
+
+const char* qr_last_error(void) { return qr::last_error(); }
+
+const char* qr_status_name(int status) {
+    switch (status) {
+        case QR_OK: return "QR_OK";
+        case QR_ERR_INVALID_ARGUMENT: return "QR_ERR_INVALID_ARGUMENT";
+        case QR_ERR_OUT_OF_RANGE: return "QR_ERR_OUT_OF_RANGE";
+        case QR_ERR_OUT_OF_MEMORY: return "QR_ERR_OUT_OF_MEMORY";
+        case QR_ERR_HIP: return "QR_ERR_HIP";
+        case QR_ERR_NOT_RESIDENT: return "QR_ERR_NOT_RESIDENT";
+        default: return "QR_ERR_UNKNOWN";
+    }
+}
+
+int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim, int max_seq,
+                 int kv_dtype, int max_batch) {
+    clear_error();
+    QR_CHECK_ARG(out != nullptr, "null output handle pointer");
+    *out = nullptr;
+    QR_CHECK_ARG(layers >= 1, "layers must be >= 1 (got %d)", layers);
+    QR_CHECK_ARG(heads >= 1 && kv_heads >= 1 && kv_heads <= heads,
+                 "need 1 <= kv_heads <= heads (got heads=%d kv_heads=%d)", heads, kv_heads);
+    QR_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256,
+                 "head_dim %d unsupported (16, 32, 64, 128 or 256)", head_dim);
+    QR_CHECK_ARG(max_seq >= 1, "max_seq must be >= 1 (got %d)", max_seq);
+    QR_CHECK_ARG(dtype_valid(kv_dtype), "unknown kv dtype %d", kv_dtype);
+    QR_CHECK_ARG(max_batch >= 1, "max_batch must be >= 1 (got %d)", max_batch);
+    const long long pt_entries = static_cast<long long>(max_batch) * layers * ((max_seq + kPageTokens - 1) / kPageTokens);
+    QR_CHECK_ARG(pt_entries < (1LL << 31), "page table of %lld entries is too large", pt_entries);
+
+    qr_kv* kv = new (std::nothrow) qr_kv();
+    if (!kv) {
+        set_error("host allocation of the handle failed");
+        return QR_ERR_OUT_OF_MEMORY;
+    }
+    kv->layers = layers;
+    kv->heads = heads;
+    kv->kv_heads = kv_heads;
+    kv->head_dim = head_dim;
+    kv->max_seq = max_seq;
+    kv->dtype = kv_dtype;
+    kv->max_batch = max_batch;
+    kv->kv_dim = kv_heads * head_dim;
+    kv->seq_len.assign(max_batch, 0);
+    int st = QR_OK;
+    if (hipGetDevice(&kv->device) != hipSuccess) {
+        set_error("no HIP device available");
+        st = QR_ERR_HIP;
+    }
+    if (st == QR_OK) {
+        PageGeom g{2, kv_heads, head_dim};
+        st = kv->store.init(g, kv_dtype, layers, max_batch, max_seq);
+    }
+    if (st == QR_OK && hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking) != hipSuccess) {
+        set_error("hipStreamCreateWithFlags failed");
+        st = QR_ERR_HIP;
+    }
+    if (st != QR_OK) {
+        if (kv->stream) (void)hipStreamDestroy(kv->stream);
+        delete kv;
+        return st;
+    }
+    *out = kv;
+    return QR_OK;
+}
+
+int qr_kv_destroy(qr_kv* kv) {
+    clear_error();
+    if (!kv) return QR_OK;
+    DeviceGuard dg(kv->device);
+    (void)hipStreamSynchronize(kv->stream);
+    (void)hipStreamDestroy(kv->stream);
+    delete kv;
+    return QR_OK;
+}
+
+int qr_kv_reserve(qr_kv* kv, int pages) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    DeviceGuard dg(kv->device);
+    return kv->store.reserve(pages);
+}
+
+int qr_kv_append(qr_kv* kv, int seq_id, int layer, int pos, const float* k, int k_len, const float* v,
+                 int v_len) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_TRY(check_pos(kv, pos));
+    QR_CHECK_ARG(k_len >= 0 && v_len >= 0, "negative row length");
+    QR_CHECK_ARG((k || k_len == 0) && (v || v_len == 0), "null k/v row");
+    if (k_len > kv->kv_dim || v_len > kv->kv_dim) {
+        set_error("row of %d/%d floats is longer than kv_dim=%d", k_len, v_len, kv->kv_dim);
+        return QR_ERR_OUT_OF_RANGE;
+    }
+    DeviceGuard dg(kv->device);
+    const size_t bytes = static_cast<size_t>(kv->kv_dim) * 4;
+    QR_TRY(kv->stage.ensure(2 * bytes));
+    char* st = static_cast<char*>(kv->stage.get());
+    if (k_len) QR_HIP(hipMemcpyAsync(st, k, k_len * 4, hipMemcpyHostToDevice, kv->stream));
+    if (v_len) QR_HIP(hipMemcpyAsync(st + bytes, v, v_len * 4, hipMemcpyHostToDevice, kv->stream));
+    QR_TRY(append_dev(kv, seq_id, layer, pos, 1, st, st + bytes, k_len, v_len, QR_DTYPE_F32, kv->stream));
+    QR_HIP(hipStreamSynchronize(kv->stream));
+    return QR_OK;
+}
+
+int qr_kv_append_range(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k, const void* v,
+                       int src_dtype) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
+    QR_CHECK_ARG(n >= 0, "negative row count %d", n);
+    QR_CHECK_ARG(n == 0 || (k && v), "null k/v rows");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(kv, pos0));
+    QR_TRY(check_pos(kv, pos0 + n - 1));
+    DeviceGuard dg(kv->device);
+    const size_t bytes = static_cast<size_t>(n) * kv->kv_dim * dtype_size(src_dtype);
+    QR_TRY(kv->stage.ensure(2 * bytes));
+    char* st = static_cast<char*>(kv->stage.get());
+    QR_HIP(hipMemcpyAsync(st, k, bytes, hipMemcpyHostToDevice, kv->stream));
+    QR_HIP(hipMemcpyAsync(st + bytes, v, bytes, hipMemcpyHostToDevice, kv->stream));
+    QR_TRY(append_dev(kv, seq_id, layer, pos0, n, st, st + bytes, kv->kv_dim, kv->kv_dim, src_dtype, kv->stream));
+    QR_HIP(hipStreamSynchronize(kv->stream));
+    return QR_OK;
+}
+
+int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k_dev,
+                           const void* v_dev, int src_dtype, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
+    QR_CHECK_ARG(n >= 0, "negative row count %d", n);
+    QR_CHECK_ARG(n == 0 || (k_dev && v_dev), "null k/v rows");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(kv, pos0));
+    QR_TRY(check_pos(kv, pos0 + n - 1));
+    DeviceGuard dg(kv->device);
+    return append_dev(kv, seq_id, layer, pos0, n, k_dev, v_dev, kv->kv_dim, kv->kv_dim, src_dtype,
+                      as_stream(stream));
+}
+
+int qr_kv_attention(qr_kv* kv, int seq_id, int layer, int pos, const float* q, float* attn, float scale) {
+    return qr_kv_attention_batch(kv, 1, &seq_id, layer, &pos, q, attn, scale);
+}
+
+int qr_kv_attention_batch(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos, const float* q,
+                          float* attn, float scale) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(q && attn, "null q/attn pointer");
+    std::vector<int> seq_len;
+    QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
+    DeviceGuard dg(kv->device);
+    const size_t bytes = static_cast<size_t>(n) * kv->heads * kv->head_dim * 4;
+    QR_TRY(kv->stage.ensure(2 * bytes));
+    float* dq = static_cast<float*>(kv->stage.get());
+    float* dout = reinterpret_cast<float*>(static_cast<char*>(kv->stage.get()) + bytes);
+    QR_HIP(hipMemcpyAsync(dq, q, bytes, hipMemcpyHostToDevice, kv->stream));
+    QR_TRY(decode_dev(kv, n, seq_ids, seq_len.data(), layer, dq, dout, scale, kv->stream));
+    QR_HIP(hipMemcpyAsync(attn, dout, bytes, hipMemcpyDeviceToHost, kv->stream));
+    QR_HIP(hipStreamSynchronize(kv->stream));
+    return QR_OK;
+}
+
+int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos, const float* q_dev,
+                        float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
+    std::vector<int> seq_len;
+    QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
+    DeviceGuard dg(kv->device);
+    return decode_dev(kv, n, seq_ids, seq_len.data(), layer, q_dev, attn_dev, scale, as_stream(stream));
+}
+
+namespace {
+int chunk_common(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void* q, int q_dtype,
+                 float* attn, bool q_is_dev, bool out_is_dev, float scale, hipStream_t stream) {
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(q && attn, "null q/attn pointer");
+    QR_CHECK_ARG(dtype_valid(q_dtype), "unknown q dtype %d", q_dtype);
+    QR_CHECK_ARG(nq >= 1, "nq must be >= 1 (got %d)", nq);
+    QR_TRY(check_pos(kv, pos0));
+    QR_TRY(check_pos(kv, pos0 + nq - 1));
+    QR_TRY(check_resident(kv, seq_id, layer, pos0 + nq - 1));
+    DeviceGuard dg(kv->device);
+    const size_t rowf = static_cast<size_t>(kv->heads) * kv->head_dim;
+    const size_t qbytes = nq * rowf * dtype_size(q_dtype);
+    const size_t fbytes = nq * rowf * 4;
+    // staging: [raw q (host path)] [fp32 q] [fp32 out (host path)]
+    QR_TRY(kv->stage.ensure(qbytes + 2 * fbytes + 512));
+    char* st = static_cast<char*>(kv->stage.get());
+    const void* qsrc = q;
+    if (!q_is_dev) {
+        QR_HIP(hipMemcpyAsync(st, q, qbytes, hipMemcpyHostToDevice, stream));
+        qsrc = st;
+    }
+    float* q32 = reinterpret_cast<float*>(st + ((qbytes + 255) & ~size_t(255)));
+    const float* qf = static_cast<const float*>(qsrc);
+    if (q_dtype != QR_DTYPE_F32) {
+        QR_HIP(launch_widen(qsrc, q_dtype, q32, static_cast<long long>(nq) * rowf, stream));
+        qf = q32;
+    }
+    float* dout = out_is_dev ? attn : q32 + nq * rowf;
+    std::vector<int> ids(nq, seq_id), lens(nq);
+    for (int i = 0; i < nq; ++i) lens[i] = pos0 + i + 1;
+    QR_TRY(decode_dev(kv, nq, ids.data(), lens.data(), layer, qf, dout, scale, stream));
+    if (!out_is_dev) {
+        QR_HIP(hipMemcpyAsync(attn, dout, fbytes, hipMemcpyDeviceToHost, stream));
+        QR_HIP(hipStreamSynchronize(stream));
+    }
+    return QR_OK;
+}
+}  // namespace
+
+int qr_kv_attention_chunk(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void* q, int q_dtype,
+                          float* attn, float scale) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    return chunk_common(kv, seq_id, layer, pos0, nq, q, q_dtype, attn, false, false, scale, kv->stream);
+}
+
+int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void* q_dev,
+                              int q_dtype, float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    return chunk_common(kv, seq_id, layer, pos0, nq, q_dev, q_dtype, attn_dev, true, true, scale,
+                        as_stream(stream));
+}
+
+int qr_kv_reset(qr_kv* kv, int seq_id) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    if (seq_id < 0) {
+        std::fill(kv->seq_len.begin(), kv->seq_len.end(), 0);
+        return QR_OK;
+    }
+    QR_CHECK_ARG(seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
+    kv->seq_len[seq_id] = 0;
+    return QR_OK;
+}
+
+int qr_kv_truncate(qr_kv* kv, int seq_id, int len) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(seq_id >= 0 && seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
+    if (len < kv->seq_len[seq_id]) kv->seq_len[seq_id] = len;  // PagedKvCache.cs:76
+    return QR_OK;
+}
+
+int qr_kv_seq_len(const qr_kv* kv, int seq_id, int* out) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(out, "null output pointer");
+    QR_CHECK_ARG(seq_id >= 0 && seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
+    *out = kv->seq_len[seq_id];
+    return QR_OK;
+}
+
+int qr_kv_bytes_used(const qr_kv* kv, long long* out) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = kv->store.bytes_used();
+    return QR_OK;
+}
+
+int qr_kv_bytes_per_token(const qr_kv* kv, long long* out) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = static_cast<long long>(kv->kv_dim) * dtype_size(kv->dtype) * 2 * kv->layers;
+    return QR_OK;
+}
+
+int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, void* v_out) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(n >= 0, "negative row count %d", n);
+    QR_CHECK_ARG(n == 0 || (k_out && v_out), "null output rows");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(kv, pos0));
+    QR_TRY(check_pos(kv, pos0 + n - 1));
+    QR_TRY(check_resident(kv, seq_id, layer, pos0 + n - 1));
+    DeviceGuard dg(kv->device);
+    const size_t bytes = static_cast<size_t>(n) * kv->kv_dim * dtype_size(kv->dtype);
+    QR_TRY(kv->stage.ensure(2 * bytes));
+    char* st = static_cast<char*>(kv->stage.get());
+    GatherArgs g{};
+    g.pool = kv->store.pool();
+    g.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+    g.geom = kv->store.geom();
+    g.dtype = kv->dtype;
+    g.dst[0] = st;
+    g.dst[1] = st + bytes;
+    g.pos0 = pos0;
+    g.n = n;
+    g.to_f32 = 0;
+    QR_HIP(launch_gather(g, kv->stream));
+    QR_HIP(hipMemcpyAsync(k_out, st, bytes, hipMemcpyDeviceToHost, kv->stream));
+    QR_HIP(hipMemcpyAsync(v_out, st + bytes, bytes, hipMemcpyDeviceToHost, kv->stream));
+    QR_HIP(hipStreamSynchronize(kv->stream));
+    return QR_OK;
+}
+
+}  // extern "C"

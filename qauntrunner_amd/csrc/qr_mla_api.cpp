@@ -1,0 +1,314 @@
+// qr_mla.cpp -- C ABI of the paged MLA latent cache (MlaLatentCache, MlaLatentCache.cs:10-65)
+// and of the absorbed attention over it (StreamingEngine.cs:531-568).
+#include <algorithm>
+#include <new>
+
+#include "qr_mla.hpp"
+#include "qr_store.hpp"
+
+using namespace qr;
+
+struct qr_mla {
+    int device = 0;
+    int layers = 0, kv_lora = 0, rope = 0, latent = 0, max_seq = 0, dtype = 0;
+    PagedStore store;
+    int seq_len = 0;
+    hipStream_t stream = nullptr;
+    DevBuf stage;
+    DevBuf workspace;
+};
+
+namespace {
+
+int check_handle(const qr_mla* m) {
+    if (!m) {
+        set_error("null qr_mla handle");
+        return QR_ERR_INVALID_ARGUMENT;
+    }
+    return QR_OK;
+}
+
+int check_layer(const qr_mla* m, int layer) {
+    QR_CHECK_ARG(layer >= 0 && layer < m->layers, "layer %d outside [0, %d)", layer, m->layers);
+    return QR_OK;
+}
+
+int check_pos(const qr_mla* m, int pos) {
+    if (pos < 0 || pos >= m->max_seq) {
+        set_error("position %d outside [0, max_seq=%d)", pos, m->max_seq);
+        return QR_ERR_OUT_OF_RANGE;
+    }
+    return QR_OK;
+}
+
+int check_resident(const qr_mla* m, int layer, int pos) {
+    if (!m->store.resident(0, layer, pos)) {
+        set_error("position %d of layer %d was never appended (%d pages resident)", pos, layer,
+                  m->store.pages_held(0, layer));
+        return QR_ERR_NOT_RESIDENT;
+    }
+    return QR_OK;
+}
+
+int append_dev(qr_mla* m, int layer, int pos0, int n, const void* rows, int len, int src_dtype,
+               hipStream_t stream) {
+    QR_TRY(m->store.ensure(0, layer, pos0 + n, stream));
+    AppendArgs a{};
+    a.pool = m->store.pool();
+    a.page_table = m->store.page_table_dev() + m->store.pt_offset(0, layer);
+    a.geom = m->store.geom();
+    a.dtype = m->dtype;
+    a.src[0] = rows;
+    a.src[1] = nullptr;
+    a.row_len[0] = len;
+    a.row_len[1] = 0;
+    a.src_stride = m->latent;
+    a.src_dtype = src_dtype;
+    a.pos0 = pos0;
+    a.n = n;
+    QR_HIP(launch_append(a, stream));
+    m->seq_len = std::max(m->seq_len, pos0 + n);  // MlaLatentCache.cs:50
+    return QR_OK;
+}
+
+int attention_dev(qr_mla* m, int layer, int pos, int heads, const float* qt, const float* qr_,
+                  float scale, float* u, hipStream_t stream) {
+    MlaArgs a{};
+    a.pool = m->store.pool();
+    a.page_table = m->store.page_table_dev() + m->store.pt_offset(0, layer);
+    a.dtype = m->dtype;
+    a.kv_lora = m->kv_lora;
+    a.rope = m->rope;
+    a.heads = heads;
+    a.seq_len = pos + 1;
+    a.q_tilde = qt;
+    a.q_rope = qr_;
+    a.u = u;
+    a.scale = scale;
+    const MlaPlan plan = plan_mla(a);
+    QR_TRY(m->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+    QR_HIP(launch_mla(a, plan, m->workspace.get(), stream));
+    return QR_OK;
+}
+
+int validate_attention(const qr_mla* m, int layer, int pos, int heads) {
+    QR_TRY(check_layer(m, layer));
+    QR_TRY(check_pos(m, pos));
+    QR_TRY(check_resident(m, layer, pos));
+    QR_CHECK_ARG(heads >= 1 && heads <= kMlaMaxHeads, "heads %d outside [1, %d]", heads, kMlaMaxHeads);
+    return QR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, int dtype) {
+    clear_error();
+    QR_CHECK_ARG(out != nullptr, "null output handle pointer");
+    *out = nullptr;
+    QR_CHECK_ARG(layers >= 1, "layers must be >= 1 (got %d)", layers);
+    QR_CHECK_ARG(kv_lora >= 64 && kv_lora <= kMlaMaxLora && kv_lora % 64 == 0,
+                 "kv_lora %d unsupported (multiple of 64, <= %d)", kv_lora, kMlaMaxLora);
+    QR_CHECK_ARG(rope >= 0 && rope <= kMlaMaxRope && rope % 16 == 0,
+                 "rope %d unsupported (multiple of 16, <= %d)", rope, kMlaMaxRope);
+    QR_CHECK_ARG(max_seq >= 1, "max_seq must be >= 1 (got %d)", max_seq);
+    QR_CHECK_ARG(dtype_valid(dtype), "unknown dtype %d", dtype);
+    qr_mla* m = new (std::nothrow) qr_mla();
+    if (!m) {
+        set_error("host allocation of the handle failed");
+        return QR_ERR_OUT_OF_MEMORY;
+    }
+    m->layers = layers;
+    m->kv_lora = kv_lora;
+    m->rope = rope;
+    m->latent = kv_lora + rope;
+    m->max_seq = max_seq;
+    m->dtype = dtype;
+    int st = QR_OK;
+    if (hipGetDevice(&m->device) != hipSuccess) {
+        set_error("no HIP device available");
+        st = QR_ERR_HIP;
+    }
+    if (st == QR_OK) {
+        PageGeom g{1, 1, m->latent};
+        st = m->store.init(g, dtype, layers, 1, max_seq);
+    }
+    if (st == QR_OK && hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+        set_error("hipStreamCreateWithFlags failed");
+        st = QR_ERR_HIP;
+    }
+    if (st != QR_OK) {
+        if (m->stream) (void)hipStreamDestroy(m->stream);
+        delete m;
+        return st;
+    }
+    *out = m;
+    return QR_OK;
+}
+
+int qr_mla_destroy(qr_mla* m) {
+    clear_error();
+    if (!m) return QR_OK;
+    DeviceGuard dg(m->device);
+    (void)hipStreamSynchronize(m->stream);
+    (void)hipStreamDestroy(m->stream);
+    delete m;
+    return QR_OK;
+}
+
+int qr_mla_reserve(qr_mla* m, int pages) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    DeviceGuard dg(m->device);
+    return m->store.reserve(pages);
+}
+
+int qr_mla_append(qr_mla* m, int layer, int pos, const float* latent, int len) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_TRY(check_pos(m, pos));
+    QR_CHECK_ARG(len >= 0 && (latent || len == 0), "null latent row");
+    if (len > m->latent) {
+        set_error("row of %d floats is longer than the latent width %d", len, m->latent);
+        return QR_ERR_OUT_OF_RANGE;
+    }
+    DeviceGuard dg(m->device);
+    QR_TRY(m->stage.ensure(static_cast<size_t>(m->latent) * 4));
+    if (len) QR_HIP(hipMemcpyAsync(m->stage.get(), latent, len * 4, hipMemcpyHostToDevice, m->stream));
+    QR_TRY(append_dev(m, layer, pos, 1, m->stage.get(), len, QR_DTYPE_F32, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+int qr_mla_append_range(qr_mla* m, int layer, int pos0, int n, const void* rows, int src_dtype) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
+    QR_CHECK_ARG(n >= 0 && (rows || n == 0), "null rows / negative count");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(m, pos0));
+    QR_TRY(check_pos(m, pos0 + n - 1));
+    DeviceGuard dg(m->device);
+    const size_t bytes = static_cast<size_t>(n) * m->latent * dtype_size(src_dtype);
+    QR_TRY(m->stage.ensure(bytes));
+    QR_HIP(hipMemcpyAsync(m->stage.get(), rows, bytes, hipMemcpyHostToDevice, m->stream));
+    QR_TRY(append_dev(m, layer, pos0, n, m->stage.get(), m->latent, src_dtype, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+int qr_mla_append_range_dev(qr_mla* m, int layer, int pos0, int n, const void* rows_dev, int src_dtype,
+                            void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
+    QR_CHECK_ARG(n >= 0 && (rows_dev || n == 0), "null rows / negative count");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(m, pos0));
+    QR_TRY(check_pos(m, pos0 + n - 1));
+    DeviceGuard dg(m->device);
+    return append_dev(m, layer, pos0, n, rows_dev, m->latent, src_dtype, static_cast<hipStream_t>(stream));
+}
+
+int qr_mla_attention(qr_mla* m, int layer, int pos, int heads, const float* q_tilde, const float* q_rope,
+                     float scale, float* u) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(q_tilde && u && (q_rope || m->rope == 0), "null q_tilde/q_rope/u pointer");
+    QR_TRY(validate_attention(m, layer, pos, heads));
+    DeviceGuard dg(m->device);
+    const size_t qt_bytes = static_cast<size_t>(heads) * m->kv_lora * 4;
+    const size_t qr_bytes = static_cast<size_t>(heads) * m->rope * 4;
+    QR_TRY(m->stage.ensure(2 * qt_bytes + qr_bytes + 512));
+    char* st = static_cast<char*>(m->stage.get());
+    float* dqt = reinterpret_cast<float*>(st);
+    float* du = reinterpret_cast<float*>(st + qt_bytes);
+    float* dqr = reinterpret_cast<float*>(st + 2 * qt_bytes);
+    QR_HIP(hipMemcpyAsync(dqt, q_tilde, qt_bytes, hipMemcpyHostToDevice, m->stream));
+    if (qr_bytes) QR_HIP(hipMemcpyAsync(dqr, q_rope, qr_bytes, hipMemcpyHostToDevice, m->stream));
+    QR_TRY(attention_dev(m, layer, pos, heads, dqt, dqr, scale, du, m->stream));
+    QR_HIP(hipMemcpyAsync(u, du, qt_bytes, hipMemcpyDeviceToHost, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+int qr_mla_attention_dev(qr_mla* m, int layer, int pos, int heads, const float* q_tilde_dev,
+                         const float* q_rope_dev, float scale, float* u_dev, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(q_tilde_dev && u_dev && (q_rope_dev || m->rope == 0), "null q_tilde/q_rope/u pointer");
+    QR_TRY(validate_attention(m, layer, pos, heads));
+    DeviceGuard dg(m->device);
+    return attention_dev(m, layer, pos, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
+                         static_cast<hipStream_t>(stream));
+}
+
+int qr_mla_reset(qr_mla* m) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    m->seq_len = 0;
+    return QR_OK;
+}
+
+int qr_mla_truncate(qr_mla* m, int len) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    if (len < m->seq_len) m->seq_len = len;  // MlaLatentCache.cs:57
+    return QR_OK;
+}
+
+int qr_mla_seq_len(const qr_mla* m, int* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = m->seq_len;
+    return QR_OK;
+}
+
+int qr_mla_bytes_used(const qr_mla* m, long long* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = m->store.bytes_used();
+    return QR_OK;
+}
+
+int qr_mla_page_count(const qr_mla* m, int layer, int* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = m->store.pages_held(0, layer);
+    return QR_OK;
+}
+
+int qr_mla_read_page(qr_mla* m, int layer, int page, float* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(out, "null output pointer");
+    QR_CHECK_ARG(page >= 0 && page < m->store.pages_held(0, layer), "page %d outside [0, %d)", page,
+                 m->store.pages_held(0, layer));
+    DeviceGuard dg(m->device);
+    const size_t bytes = static_cast<size_t>(kPageTokens) * m->latent * 4;
+    QR_TRY(m->stage.ensure(bytes));
+    GatherArgs g{};
+    g.pool = m->store.pool();
+    g.page_table = m->store.page_table_dev() + m->store.pt_offset(0, layer);
+    g.geom = m->store.geom();
+    g.dtype = m->dtype;
+    g.dst[0] = m->stage.get();
+    g.pos0 = page * kPageTokens;
+    g.n = kPageTokens;
+    g.to_f32 = 1;
+    QR_HIP(launch_gather(g, m->stream));
+    QR_HIP(hipMemcpyAsync(out, m->stage.get(), bytes, hipMemcpyDeviceToHost, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,83 @@
+// qr_store.hpp -- HBM page pool + device page tables shared by the KV and MLA caches.
+#pragma once
+
+#include <vector>
+
+#include "qr_kernels.hpp"
+
+namespace qr {
+
+// Makes the handle's device current for the duration of a call.
+class DeviceGuard {
+public:
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    }
+    bool ok() const { return ok_; }
+
+private:
+    int prev_ = -1;
+    bool ok_ = true;
+};
+
+// Growable device buffer.  Growing waits for the device to go idle first,
+// because work enqueued on any stream may still read the old allocation.
+class DevBuf {
+public:
+    ~DevBuf() { if (ptr_) (void)hipFree(ptr_); }
+    int ensure(size_t bytes);
+    void* get() const { return ptr_; }
+    size_t size() const { return size_; }
+
+private:
+    void* ptr_ = nullptr;
+    size_t size_ = 0;
+};
+
+// Page pool of one cache: `seqs` sequences x `layers` layers, each with a row
+// of `max_pages` page-table entries.  A page is allocated when any of its
+// positions is first appended (the intended behaviour of PagedKvCache.Ensure,
+// PagedKvCache.cs:41-60; every page up to the appended one is allocated) and
+// is zero-filled at allocation, as a fresh managed array is.
+class PagedStore {
+public:
+    ~PagedStore();
+    int init(const PageGeom& geom, int dtype, int layers, int seqs, int max_seq);
+    // Makes positions 0..tokens-1 of (seq, layer) resident; uploads new page-table entries.
+    int ensure(int seq, int layer, int tokens, hipStream_t stream);
+    int reserve(int pages);
+
+    int pages_held(int seq, int layer) const { return held_[static_cast<size_t>(seq) * layers_ + layer]; }
+    bool resident(int seq, int layer, int pos) const {
+        return static_cast<long long>(pages_held(seq, layer)) * kPageTokens > pos;
+    }
+    int pt_offset(int seq, int layer) const { return (seq * layers_ + layer) * max_pages_; }
+    const int* page_table_dev() const { return pt_dev_; }
+    void* pool() const { return pool_; }
+    const PageGeom& geom() const { return geom_; }
+    int dtype() const { return dtype_; }
+    long long page_bytes() const { return geom_.page_elems() * dtype_size(dtype_); }
+    long long bytes_used() const { return pages_used_ * page_bytes(); }
+    int max_pages() const { return max_pages_; }
+
+private:
+    int grow(long long min_pages);
+    int grow_done(char* fresh, long long cap, size_t page_bytes);
+
+    PageGeom geom_{};
+    int dtype_ = QR_DTYPE_F32;
+    int layers_ = 0, seqs_ = 0, max_pages_ = 0;
+    char* pool_ = nullptr;
+    long long pool_cap_ = 0;   // pages allocated in the pool
+    long long pages_used_ = 0; // pages handed out
+    std::vector<int> pt_host_;
+    int* pt_dev_ = nullptr;
+    std::vector<int> held_;
+};
+
+}  // namespace qr

@@ -1,0 +1,72 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point the
+header declares, and rejects invalid arguments before touching a device."""
+import ctypes
+import re
+
+import pytest
+
+import qauntrunner_amd as qr
+from qauntrunner_amd import _lib
+
+
+def declared_functions():
+    text = open(_lib.HEADER_PATH).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\s*\*)\s+(qr_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_status_names():
+    L = qr.load()
+    assert L.qr_abi_version() == 1
+    assert L.qr_status_name(0) == b"QR_OK"
+    assert L.qr_status_name(-2) == b"QR_ERR_OUT_OF_RANGE"
+    assert L.qr_status_name(-5) == b"QR_ERR_NOT_RESIDENT"
+    assert L.qr_status_name(-99) == b"QR_ERR_UNKNOWN"
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((0, 8, 2, 64, 512, 0, 1), "layers"),
+    ((1, 2, 4, 64, 512, 0, 1), "kv_heads"),
+    ((1, 8, 2, 48, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 64, 0, 0, 1), "max_seq"),
+    ((1, 8, 2, 64, 512, 7, 1), "dtype"),
+    ((1, 8, 2, 64, 512, 0, 0), "max_batch"),
+])
+def test_kv_create_validates_before_device(args, needle):
+    L = qr.load()
+    h = ctypes.c_void_p()
+    st = L.qr_kv_create(ctypes.byref(h), *args)
+    assert st == _lib.QR_ERR_INVALID_ARGUMENT and not h.value
+    assert needle in L.qr_last_error().decode()
+
+
+@pytest.mark.parametrize("args", [(0, 512, 64, 100, 2), (1, 500, 64, 100, 2), (1, 512, 60, 100, 2), (1, 512, 64, 100, 9)])
+def test_mla_create_validates_before_device(args):
+    L = qr.load()
+    h = ctypes.c_void_p()
+    assert L.qr_mla_create(ctypes.byref(h), *args) == _lib.QR_ERR_INVALID_ARGUMENT and not h.value
+
+
+def test_null_handles_are_rejected():
+    L = qr.load()
+    out = ctypes.c_int()
+    assert L.qr_kv_seq_len(None, 0, ctypes.byref(out)) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_attention(None, 0, 0, 0, None, None, 1.0) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_attention(None, 0, 0, 1, None, None, 1.0, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_destroy(None) == 0 and L.qr_mla_destroy(None) == 0
+    assert "null" in L.qr_last_error().decode() or L.qr_last_error() == b""
+
+
+def test_status_maps_to_python_exceptions():
+    with pytest.raises(qr.QrInvalidArgument):
+        qr.PagedKvCache(1, 8, 2, 48, 512)
+    assert issubclass(qr.QrOutOfRange, IndexError) and issubclass(qr.QrNotResident, LookupError)
