@@ -123,6 +123,12 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
                               const void* q_dev, int q_dtype, float* attn_dev, float scale,
                               void* stream);
 
+/* Benchmark instrumentation, no reference counterpart: when `event` (a
+ * hipEvent_t) is not NULL, every later attention call records it on its
+ * stream right after the split-K kernel and before the combine kernel, so a
+ * caller can time the split-K kernel alone.  NULL turns it off. */
+int qr_kv_set_split_event(qr_kv* kv, void* event);
+
 /* Reset(), PagedKvCache.cs:72 (seq_id < 0 resets every sequence). */
 int qr_kv_reset(qr_kv* kv, int seq_id);
 /* Truncate(len), PagedKvCache.cs:76: SeqLen = min(SeqLen, len). */

@@ -105,6 +105,10 @@ class PagedKvCache:
     def Reserve(self, pages: int) -> None:
         check(self._lib.qr_kv_reserve(self._h, pages))
 
+    def SetSplitEvent(self, event) -> None:
+        """Benchmark instrumentation: record hipEvent_t `event` after every split-K kernel (None: off)."""
+        check(self._lib.qr_kv_set_split_event(self._h, event))
+
     # ---- writes
     def Append(self, layer, pos, k, v, seq_id=0) -> None:
         """PagedKvCache.Append (:62-69): fp32 rows of at most kv_dim floats."""

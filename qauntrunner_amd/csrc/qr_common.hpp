@@ -107,7 +107,7 @@ __device__ __forceinline__ float dpp_half_mirror(float v) { return dpp_mov<0x141
 // row_mirror: lane i <-> 15-i inside each row of 16 (swaps the two halves)
 __device__ __forceinline__ float dpp_mirror(float v) { return dpp_mov<0x140>(v); }
 
-// Sum over aligned groups of `lanes` consecutive lanes (1, 2, 4, 8 or 16).
+// Sum over aligned groups of `lanes` consecutive lanes (1, 2, 4, 8, 16 or 32).
 // Every lane of a group ends with the bit-identical group sum, because each
 // step adds the same two operands in every lane (IEEE addition commutes).
 __device__ __forceinline__ float group_sum(float x, int lanes) {
@@ -115,6 +115,7 @@ __device__ __forceinline__ float group_sum(float x, int lanes) {
     if (lanes >= 4) x += dpp_xor2(x);
     if (lanes >= 8) x += dpp_half_mirror(x);
     if (lanes >= 16) x += dpp_mirror(x);
+    if (lanes >= 32) x += __shfl_xor(x, 16);
     return x;
 }
 

@@ -1,37 +1,49 @@
 // qr_decode.hip -- split-K (flash-decoding) GQA decode attention for gfx950.
 //
 // Replaces the two-pass, fully materialised PagedKvCache.Attention
-// (PagedKvCache.cs:83-136) with:
-//   decode_split_kernel   one workgroup per (entry, kv head [x head chunk], split of
-//                         split_tokens positions).  K/V rows of the split are read
-//                         from HBM once and shared by every query head of the group.
-//   decode_combine_kernel log-sum-exp merge of the per-split partials.
+// (PagedKvCache.cs:83-136) with decode_stream_kernel + decode_combine_kernel.
+//
+// Grid: (split, unit, entry).  A unit is one kv head with up to GMAX of its
+// query heads (or one query head when kv_heads does not divide heads).  A
+// split is a run of whole pages of one entry; every K/V row of the split is
+// read from HBM exactly once and shared by all query heads of the unit.
 //
 // Lane layout (wave64): a token row of head_dim elements is spread over
-// LPT = head_dim/16 consecutive lanes, 16 elements per lane, taken as 16-byte
+// LPT = head_dim/8 consecutive lanes, 8 elements per lane, taken as 16-byte
 // chunks c = sub + LPT*j (sub = lane % LPT).  One load instruction of a wave
-// therefore reads LPT*16 contiguous bytes from each of 64/LPT consecutive rows;
-// rows of one (page, kv head) are contiguous, so a wave reads one contiguous run.
-// Per-token dot products are finished with DPP butterflies inside the LPT lanes.
+// reads LPT*16 contiguous bytes from each of 64/LPT consecutive rows, and the
+// rows of one (page, kv head) are contiguous in the pool, so every wave load
+// is a single contiguous run.  Dot products finish with DPP butterflies
+// inside the LPT lanes of a token.
 //
-// Softmax: each token group (the LPT lanes that share a token stream) keeps
-// its T scores per head in registers, takes their max, exponentiates relative
-// to it and accumulates p*V.  Token groups, waves and splits are then merged
-// with the log-sum-exp rule, so no accumulator is rescaled inside the stream.
-// Scores are kept in log2 units: q is pre-multiplied by scale*log2(e) and
-// exponentials use v_exp_f32 (exp2).
+// Streaming: the workgroup walks its split in steps of U*256/LPT consecutive
+// positions (U = 2 rows per token group for fp32, 4 for 16-bit, so a step is
+// 32 KB of K+V at head_dim >= 32).  The K/V chunks of the next kPrefetch steps
+// are already in flight in registers while a step is computed, so HBM sees
+// a steady queue without any LDS staging of the stream.
+//
+// Softmax: online, in log2 units (q is pre-multiplied by scale*log2(e) and
+// exponentials are v_exp_f32).  Each token group keeps its own running max
+// and rescales its accumulator only when that max grows, which becomes rare
+// after the first steps; no lane exchange sits inside the stream.  Token
+// groups, waves, then splits are merged with the log-sum-exp rule.
+// decode_combine_kernel then merges the splits of every (entry, head); an
+// entry covered by a single split is written directly by the split kernel.
 #include "qr_kernels.hpp"
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <type_traits>
 
 namespace qr {
 namespace {
 
-constexpr int kWaves = 4;            // waves per workgroup
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kTokensPerGroup = 8;   // T: tokens each token group handles per split
-constexpr int kMaxCombineSplits = 4096;
+constexpr int kPrefetch = 2;        // steps in flight beyond the one being computed (3 buffers)
+constexpr int kMaxSplits = 256;     // splits per (entry, unit) merged by the last workgroup
+constexpr int kMaxGroup = 8;        // GMAX upper bound
 
 struct DecodeK {
     const char* pool;
@@ -44,14 +56,14 @@ struct DecodeK {
     int heads;
     int group;           // heads / kv_heads (uniform GQA)
     int head_chunks;     // ceil(group / GMAX)
-    int per_head;        // 1: one query head per workgroup (kv_heads does not divide heads)
+    int per_head;        // 1: one query head per unit (kv_heads does not divide heads)
+    int units;
     const float* q;
     float* out;
-    float* part_acc;     // [nb][heads][max_splits][head_dim]
-    float2* part_ml;     // [nb][heads][max_splits] (max in log2 units, sum)
+    float* part_acc;     // [nb][heads][kMaxSplits][head_dim]
+    float2* part_ml;     // [nb][heads][kMaxSplits] (max in log2 units, sum)
     float qscale;        // scale * log2(e)
     int split_tokens;
-    int max_splits;
     int seq_len[kMaxDecodeBatch];
     int pt_off[kMaxDecodeBatch];
 };
@@ -60,12 +72,14 @@ __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
 }
 
-template <typename KT, int GMAX, int T>
-__global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p) {
+// DT: head_dim fixed at compile time (0: read from the arguments).
+template <typename KT, int GMAX, int DPL, int U, int DT>
+__global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p) {
     using C = Chunk<KT>;
     constexpr int EPC = C::kElems;  // elements per 16-byte chunk
-    constexpr int NC = 16 / EPC;    // chunks per lane
+    constexpr int NC = DPL / EPC;   // chunks per lane per row
     constexpr int ESZ = 16 / EPC;   // bytes per element
+    constexpr int UMAX = U;         // rows per token group per step
 
     const int split = blockIdx.x;
     const int unit = blockIdx.y;
@@ -75,8 +89,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
     if (t_begin >= seq) return;
     const int t_end = min(seq, t_begin + p.split_tokens);
 
-    const int D = p.head_dim;
-    const int lsh = p.lpt_shift;
+    const int D = DT ? DT : p.head_dim;
+    const int lsh = DT ? __builtin_ctz(DT / DPL) : p.lpt_shift;
     const int LPT = 1 << lsh;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -84,6 +98,7 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
     const int tpw = 64 >> lsh;
     const int ntg = kWaves * tpw;
     const int tg = wave * tpw + (lane >> lsh);
+    const int step_tokens = U * ntg;
 
     int kvh, h0, G;
     if (p.per_head) {
@@ -97,8 +112,103 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
         G = min(GMAX, p.group - c * GMAX);
     }
 
-    // ---- query slice of this lane, pre-scaled into log2 units
-    float q[GMAX][16];
+    float q[GMAX][DPL];  // filled once the first K/V step is in flight
+    const int* pt = p.page_table + p.pt_off[b];
+    const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
+    const int row_in_step = tg;  // + u * ntg
+    const int nsteps = (t_end - t_begin + step_tokens - 1) / step_tokens;
+
+    // chunk c of the K (plane 0) or V (plane 1) row `slot` of physical page `phys`
+    auto row_ptr = [&](long long phys, int plane, int slot) -> const char* {
+        return p.pool + (phys * p.page_elems + plane * p.plane_elems + head_off +
+                         static_cast<long long>(slot) * D) * ESZ;
+    };
+
+    U32x4 kbuf[kPrefetch + 1][UMAX][NC];
+    U32x4 vbuf[kPrefetch + 1][UMAX][NC];
+    auto issue = [&](int st, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
+        const int t0 = t_begin + st * step_tokens;       // uniform: a step never crosses a page
+        const long long phys = pt[t0 >> kPageShift];
+        const int slot0 = (t0 & (kPageTokens - 1)) + row_in_step;
+#pragma unroll
+        for (int u = 0; u < UMAX; ++u) {
+            const char* kr = row_ptr(phys, 0, slot0 + u * ntg);
+            const char* vr = row_ptr(phys, 1, slot0 + u * ntg);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) kb[u][j] = load16(kr + (sub + LPT * j) * 16);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) vb[u][j] = load16(vr + (sub + LPT * j) * 16);
+        }
+    };
+
+    float m[GMAX], l[GMAX], acc[GMAX][DPL];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
+    }
+
+    auto compute = [&](int st, const U32x4 (&kb)[UMAX][NC], const U32x4 (&vb)[UMAX][NC]) {
+        const int t0 = t_begin + st * step_tokens + row_in_step;
+        float s[UMAX][GMAX];
+#pragma unroll
+        for (int u = 0; u < UMAX; ++u) {
+            float k[DPL];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) C::widen(kb[u][j], &k[j * EPC]);
+            const bool valid = t0 + u * ntg < t_end;
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) d = fmaf(q[g][e], k[e], d);
+                d = group_sum(d, LPT);
+                s[u][g] = valid ? d : -INFINITY;
+            }
+        }
+        // running max of this token group (equal in its LPT lanes); the accumulator
+        // is rescaled only in lanes whose max grows
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            float smax = s[0][g];
+#pragma unroll
+            for (int u = 1; u < UMAX; ++u) smax = fmaxf(smax, s[u][g]);
+            if (smax > m[g]) {
+                const float corr = exp2_or_zero(m[g] - smax, m[g]);
+                l[g] *= corr;
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) acc[g][e] *= corr;
+                m[g] = smax;
+            }
+        }
+        // a token group that has seen only masked rows still has m = -inf: weigh them 0, not NaN
+        float mref[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) mref[g] = m[g] == -INFINITY ? 0.f : m[g];
+#pragma unroll
+        for (int u = 0; u < UMAX; ++u) {
+            float v[DPL];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) C::widen(vb[u][j], &v[j * EPC]);
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                const float pr = fast_exp2(s[u][g] - mref[g]);  // masked rows: exp2(-inf) = 0
+                l[g] += pr;
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pr, v[e], acc[g][e]);
+            }
+        }
+    };
+
+    // ---- software-pipelined stream over the split.  Every step issues the same
+    // number of loads (past the end it re-reads the step just computed, which
+    // L2 still holds), so the compiler's load counting stays exact and each
+    // step waits only for its own loads.
+    issue(0, kbuf[0], vbuf[0]);
+    // ---- query slice of this lane, pre-scaled into log2 units (loaded after the
+    // first K/V step is in flight, so the two latencies overlap)
     const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
 #pragma unroll
     for (int g = 0; g < GMAX; ++g)
@@ -107,74 +217,24 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
 #pragma unroll
             for (int e = 0; e < EPC; ++e) {
                 const int dim = (sub + LPT * j) * EPC + e;
-                q[g][j * EPC + e] = (g < G) ? qb[static_cast<size_t>(h0 + g) * D + dim] * p.qscale : 0.f;
+                const int h = min(h0 + g, p.heads - 1);  // rows past the unit's heads are read, then zeroed
+                q[g][j * EPC + e] = qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f);
             }
 
-    const int* pt = p.page_table + p.pt_off[b];
-    const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
-
-    // ---- scores of this token group's T positions
-    float s[T][GMAX];
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const int t = t_begin + tg + i * ntg;
-        const bool valid = t < t_end;
-        const int tc = valid ? t : t_end - 1;
-        const long long phys = pt[tc >> kPageShift];
-        const char* row = p.pool + (phys * p.page_elems + head_off +
-                                    static_cast<long long>(tc & (kPageTokens - 1)) * D) * ESZ;
-        float k[16];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) C::widen(load16(row + (sub + LPT * j) * 16), &k[j * EPC]);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) d = fmaf(q[g][e], k[e], d);
-            d = group_sum(d, LPT);
-            s[i][g] = valid ? d : -INFINITY;
-        }
+    issue(min(1, nsteps - 1), kbuf[1], vbuf[1]);
+    for (int s0 = 0;; s0 += 3) {  // exits only through the breaks: the back-edge is steady state
+        issue(s0 + 2 < nsteps ? s0 + 2 : s0, kbuf[2], vbuf[2]);
+        compute(s0, kbuf[0], vbuf[0]);
+        if (s0 + 1 >= nsteps) break;
+        issue(s0 + 3 < nsteps ? s0 + 3 : s0 + 1, kbuf[0], vbuf[0]);
+        compute(s0 + 1, kbuf[1], vbuf[1]);
+        if (s0 + 2 >= nsteps) break;
+        issue(s0 + 4 < nsteps ? s0 + 4 : s0 + 2, kbuf[1], vbuf[1]);
+        compute(s0 + 2, kbuf[2], vbuf[2]);
+        if (s0 + 3 >= nsteps) break;
     }
 
-    // ---- local softmax numerators
-    float m[GMAX], l[GMAX];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-        m[g] = s[0][g];
-#pragma unroll
-        for (int i = 1; i < T; ++i) m[g] = fmaxf(m[g], s[i][g]);
-        const float mref = (m[g] == -INFINITY) ? 0.f : m[g];
-        l[g] = 0.f;
-#pragma unroll
-        for (int i = 0; i < T; ++i) {
-            s[i][g] = fast_exp2(s[i][g] - mref);
-            l[g] += s[i][g];
-        }
-    }
-
-    // ---- p . V
-    float acc[GMAX][16];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[g][e] = 0.f;
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const int t = t_begin + tg + i * ntg;
-        const int tc = t < t_end ? t : t_end - 1;
-        const long long phys = pt[tc >> kPageShift];
-        const char* row = p.pool + (phys * p.page_elems + p.plane_elems + head_off +
-                                    static_cast<long long>(tc & (kPageTokens - 1)) * D) * ESZ;
-        float v[16];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) C::widen(load16(row + (sub + LPT * j) * 16), &v[j * EPC]);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[g][e] = fmaf(s[i][g], v[e], acc[g][e]);
-    }
-
-    // ---- merge the token groups of this wave (lanes with equal `sub`)
+    // ---- merge the token groups of the wave (lanes with equal `sub`)
     for (int off = LPT; off < 64; off <<= 1) {
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
@@ -185,12 +245,12 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
             const float c2 = exp2_or_zero(m2 - M, m2);
             l[g] = l[g] * c1 + l2 * c2;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[g][e] = acc[g][e] * c1 + __shfl_xor(acc[g][e], off) * c2;
+            for (int e = 0; e < DPL; ++e) acc[g][e] = acc[g][e] * c1 + __shfl_xor(acc[g][e], off) * c2;
             m[g] = M;
         }
     }
 
-    // ---- merge the waves through LDS and write the split's partial
+    // ---- merge the waves through LDS
     __shared__ float sm_acc[kWaves][GMAX][256];
     __shared__ float sm_m[kWaves][GMAX];
     __shared__ float sm_l[kWaves][GMAX];
@@ -209,7 +269,8 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
     }
     __syncthreads();
 
-    const bool single = (t_begin == 0 && t_end == seq);
+    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    const size_t row_base = static_cast<size_t>(b) * p.heads;
     for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
         const int g = idx / D;
         const int d = idx - g * D;
@@ -224,18 +285,21 @@ __global__ void __launch_bounds__(kThreads) decode_split_kernel(const DecodeK p)
             o += sm_acc[w][g][d] * c;
         }
         const int h = h0 + g;
-        if (single) {
-            p.out[(static_cast<size_t>(b) * p.heads + h) * D + d] = o / L;
+        if (nsplit == 1) {
+            p.out[(row_base + h) * D + d] = o / L;
         } else {
-            const size_t slot = (static_cast<size_t>(b) * p.heads + h) * p.max_splits + split;
+            const size_t slot = (row_base + h) * kMaxSplits + split;
             p.part_acc[slot * D + d] = o;
             if (d == 0) p.part_ml[slot] = make_float2(M, L);
         }
     }
 }
 
-// One workgroup per (head, entry).  Weights of the splits go through LDS, then
-// head_dim/4 lanes x (256*4/head_dim) split groups read the partials as float4.
+// Log-sum-exp merge of the split partials: one workgroup per (head, entry).
+// Thread t owns float4 column t % (head_dim/4) and every (256*4/head_dim)-th
+// split; it loads up to 8 of its partials at once (one memory round trip for
+// up to 64 splits at head_dim 128), merges them online, and the threads of a
+// column are then merged through LDS.
 __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK p) {
     const int h = blockIdx.x;
     const int b = blockIdx.y;
@@ -243,66 +307,64 @@ __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK 
     const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
     if (nsplit <= 1) return;
     const int D = p.head_dim;
-    const size_t base = (static_cast<size_t>(b) * p.heads + h) * p.max_splits;
-
-    __shared__ float w[kMaxCombineSplits];
-    __shared__ float red[kThreads];
-    __shared__ float4 red4[kThreads];
-
-    // global max of the split maxima
-    float mx = -INFINITY;
-    for (int s = threadIdx.x; s < nsplit; s += kThreads) {
-        const float ms = p.part_ml[base + s].x;
-        w[s] = ms;
-        mx = fmaxf(mx, ms);
-    }
-    red[threadIdx.x] = mx;
-    __syncthreads();
-    for (int o = kThreads / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-        __syncthreads();
-    }
-    const float M = red[0];
-    __syncthreads();
-
-    // split weights and the total denominator
-    float lsum = 0.f;
-    for (int s = threadIdx.x; s < nsplit; s += kThreads) {
-        const float c = exp2_or_zero(w[s] - M, w[s]);
-        w[s] = c;
-        lsum += p.part_ml[base + s].y * c;
-    }
-    red[threadIdx.x] = lsum;
-    __syncthreads();
-    for (int o = kThreads / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const float L = red[0];
-
-    // weighted sum of the partial accumulators
+    const size_t base = (static_cast<size_t>(b) * p.heads + h) * kMaxSplits;
     const int d4n = D >> 2;
     const int groups = kThreads / d4n;
     const int d4 = threadIdx.x % d4n;
     const int grp = threadIdx.x / d4n;
-    float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* acc4 = reinterpret_cast<const float4*>(p.part_acc + base * D);
-#pragma unroll 8
-    for (int s = grp; s < nsplit; s += groups) {
-        const float4 a = acc4[static_cast<size_t>(s) * d4n + d4];
-        const float c = w[s];
-        o4.x = fmaf(a.x, c, o4.x);
-        o4.y = fmaf(a.y, c, o4.y);
-        o4.z = fmaf(a.z, c, o4.z);
-        o4.w = fmaf(a.w, c, o4.w);
+    const float4* acc4 = reinterpret_cast<const float4*>(p.part_acc);
+    constexpr int kBatch = 8;
+
+    float m = -INFINITY, l = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = grp; s0 < nsplit; s0 += groups * kBatch) {
+        float4 a[kBatch];
+        float2 ml[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int s = s0 + i * groups;
+            const bool in = s < nsplit;
+            a[i] = in ? acc4[(base + s) * d4n + d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ml[i] = in ? p.part_ml[base + s] : make_float2(-INFINITY, 0.f);
+        }
+        float mb = m;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) mb = fmaxf(mb, ml[i].x);
+        const float cm = exp2_or_zero(m - mb, m);
+        l *= cm;
+        o.x *= cm; o.y *= cm; o.z *= cm; o.w *= cm;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const float c = exp2_or_zero(ml[i].x - mb, ml[i].x);
+            l = fmaf(ml[i].y, c, l);
+            o.x = fmaf(a[i].x, c, o.x);
+            o.y = fmaf(a[i].y, c, o.y);
+            o.z = fmaf(a[i].z, c, o.z);
+            o.w = fmaf(a[i].w, c, o.w);
+        }
+        m = mb;
     }
-    red4[threadIdx.x] = o4;
+
+    __shared__ float red_m[kThreads];
+    __shared__ float red_l[kThreads];
+    __shared__ float4 red_o[kThreads];
+    red_m[threadIdx.x] = m;
+    red_l[threadIdx.x] = l;
+    red_o[threadIdx.x] = o;
     __syncthreads();
     if (threadIdx.x < d4n) {
-        float4 t = red4[threadIdx.x];
-        for (int gi = 1; gi < groups; ++gi) {
-            const float4 u = red4[gi * d4n + threadIdx.x];
-            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        float M = -INFINITY;
+        for (int gi = 0; gi < groups; ++gi) M = fmaxf(M, red_m[gi * d4n + threadIdx.x]);
+        float L = 0.f;
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int gi = 0; gi < groups; ++gi) {
+            const int k = gi * d4n + threadIdx.x;
+            const float c = exp2_or_zero(red_m[k] - M, red_m[k]);
+            L = fmaf(red_l[k], c, L);
+            t.x = fmaf(red_o[k].x, c, t.x);
+            t.y = fmaf(red_o[k].y, c, t.y);
+            t.z = fmaf(red_o[k].z, c, t.z);
+            t.w = fmaf(red_o[k].w, c, t.w);
         }
         float* out = p.out + (static_cast<size_t>(b) * p.heads + h) * D + threadIdx.x * 4;
         out[0] = t.x / L;
@@ -316,24 +378,7 @@ int pick_gmax(int group) {
     if (group <= 1) return 1;
     if (group <= 2) return 2;
     if (group <= 4) return 4;
-    return 8;
-}
-
-template <typename KT, int GMAX>
-hipError_t launch_split(const DecodeK& k, dim3 grid, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_split_kernel<KT, GMAX, kTokensPerGroup>), grid, dim3(kThreads), 0,
-                       stream, k);
-    return hipGetLastError();
-}
-
-template <typename KT>
-hipError_t dispatch_gmax(int gmax, const DecodeK& k, dim3 grid, hipStream_t stream) {
-    switch (gmax) {
-        case 1: return launch_split<KT, 1>(k, grid, stream);
-        case 2: return launch_split<KT, 2>(k, grid, stream);
-        case 4: return launch_split<KT, 4>(k, grid, stream);
-        default: return launch_split<KT, 8>(k, grid, stream);
-    }
+    return kMaxGroup;
 }
 
 int log2_exact(int v) {
@@ -342,46 +387,126 @@ int log2_exact(int v) {
     return s;
 }
 
+constexpr int kDimsPerLane = 8;
+
+
+template <typename KT, int GMAX, int U, int DT>
+const void* kernel_ptr() {
+    return reinterpret_cast<const void*>(&decode_stream_kernel<KT, GMAX, kDimsPerLane, U, DT>);
+}
+
+template <typename KT, int U, int DT>
+const void* by_gmax(int gmax) {
+    return gmax == 1 ? kernel_ptr<KT, 1, U, DT>() : gmax == 2 ? kernel_ptr<KT, 2, U, DT>()
+         : gmax == 4 ? kernel_ptr<KT, 4, U, DT>() : kernel_ptr<KT, 8, U, DT>();
+}
+
+// A step is 32 KB of K+V: 2 fp32 or 4 16-bit rows per token group.  At head_dim
+// 16 a step of 4 16-bit rows would cross a page, so it takes 2.  head_dim 64
+// and 128 get instances with the dimension fixed at compile time.
+template <typename KT, int U>
+const void* by_dim(int gmax, int head_dim) {
+    return head_dim == 128 ? by_gmax<KT, U, 128>(gmax) : head_dim == 64 ? by_gmax<KT, U, 64>(gmax)
+         : by_gmax<KT, U, 0>(gmax);
+}
+
+const void* select_kernel(int dtype, int gmax, int head_dim) {
+    const bool narrow = head_dim == 16;
+    switch (dtype) {
+        case QR_DTYPE_F32: return by_dim<float, 2>(gmax, head_dim);
+        case QR_DTYPE_F16: return narrow ? by_gmax<F16Tag, 2, 0>(gmax) : by_dim<F16Tag, 4>(gmax, head_dim);
+        default: return narrow ? by_gmax<BF16Tag, 2, 0>(gmax) : by_dim<BF16Tag, 4>(gmax, head_dim);
+    }
+}
+
+// Resident workgroups per CU of a kernel instance (queried once per instance).
+int blocks_per_cu(const void* fn) {
+    static std::mutex mu;
+    static const void* keys[64];
+    static int vals[64];
+    static int n = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n; ++i)
+        if (keys[i] == fn) return vals[i];
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, 0) != hipSuccess || blocks < 1) {
+        (void)hipGetLastError();
+        blocks = 1;
+    }
+    if (n < 64) {
+        keys[n] = fn;
+        vals[n] = blocks;
+        ++n;
+    }
+    return blocks;
+}
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+            cus = prop.multiProcessorCount;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+int units_of(const DecodeArgs& a, int* gmax) {
+    const int kvh = a.geom.kv_heads;
+    if (a.heads % kvh == 0) {
+        const int group = a.heads / kvh;
+        *gmax = pick_gmax(group);
+        return kvh * ((group + *gmax - 1) / *gmax);
+    }
+    *gmax = 1;
+    return a.heads;
+}
+
 }  // namespace
 
 DecodePlan plan_decode(const DecodeArgs& a) {
     DecodePlan pl{};
-    const int D = a.geom.head_dim;
-    const int lpt = D / 16;
-    const int ntg = kWaves * (64 / lpt);
-    pl.split_tokens = kTokensPerGroup * ntg;
-    int max_len = 0;
-    for (int i = 0; i < a.nb; ++i) max_len = std::max(max_len, a.seq_len[i]);
-    pl.max_splits = std::max(1, (max_len + pl.split_tokens - 1) / pl.split_tokens);
-    const int kvh = a.geom.kv_heads;
-    if (a.heads % kvh == 0) {
-        const int group = a.heads / kvh;
-        const int gmax = pick_gmax(group);
-        pl.units = kvh * ((group + gmax - 1) / gmax);
-    } else {
-        pl.units = a.heads;
+    int gmax = 1;
+    pl.units = units_of(a, &gmax);
+    int max_pages = 1;
+    long long work = 0;  // (unit, page) items of the launch
+    for (int i = 0; i < a.nb; ++i) {
+        const int pages = (a.seq_len[i] + kPageTokens - 1) / kPageTokens;
+        max_pages = std::max(max_pages, pages);
+        work += static_cast<long long>(pages) * pl.units;
     }
+    // about one workgroup per CU, whole pages per split, at most 16 pages per split
+    // (measured on MI355X: fewer, longer splits beat more resident workgroups)
+    (void)blocks_per_cu;
+    long long pps = std::max<long long>(1, work / cu_count());
+    pps = std::min<long long>(pps, 16);
+    pps = std::max<long long>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
+    pps = std::min<long long>(pps, max_pages);
+    pl.split_tokens = static_cast<int>(pps) * kPageTokens;
+    pl.max_splits = (max_pages + static_cast<int>(pps) - 1) / static_cast<int>(pps);
     pl.workspace_bytes = pl.max_splits > 1
-        ? static_cast<size_t>(a.nb) * a.heads * pl.max_splits * (static_cast<size_t>(D) * 4 + 8)
+        ? static_cast<size_t>(a.nb) * a.heads * kMaxSplits * (static_cast<size_t>(a.geom.head_dim) * 4 + 8)
         : 0;
     return pl;
 }
 
-hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* workspace,
-                         hipStream_t stream) {
+hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* workspace, hipStream_t stream,
+                         hipEvent_t after_split) {
     DecodeK k{};
+    int gmax = 1;
+    k.units = units_of(a, &gmax);
     k.pool = static_cast<const char*>(a.pool);
     k.page_table = a.page_table;
     k.page_elems = a.geom.page_elems();
     k.plane_elems = a.geom.plane_elems();
     k.head_dim = a.geom.head_dim;
-    k.lpt_shift = log2_exact(a.geom.head_dim / 16);
+    k.lpt_shift = log2_exact(a.geom.head_dim / kDimsPerLane);
     k.kv_heads = a.geom.kv_heads;
     k.heads = a.heads;
-    int gmax = 1;
     if (a.heads % a.geom.kv_heads == 0) {
         k.group = a.heads / a.geom.kv_heads;
-        gmax = pick_gmax(k.group);
         k.head_chunks = (k.group + gmax - 1) / gmax;
         k.per_head = 0;
     } else {
@@ -391,26 +516,22 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
     }
     k.q = a.q;
     k.out = a.out;
-    const size_t slots = static_cast<size_t>(a.nb) * a.heads * pl.max_splits;
+    const size_t slots = static_cast<size_t>(a.nb) * a.heads * kMaxSplits;
     k.part_acc = static_cast<float*>(workspace);
     k.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + slots * a.geom.head_dim * 4);
     k.qscale = static_cast<float>(static_cast<double>(a.scale) * 1.4426950408889634);
     k.split_tokens = pl.split_tokens;
-    k.max_splits = pl.max_splits;
     for (int i = 0; i < a.nb; ++i) {
         k.seq_len[i] = a.seq_len[i];
         k.pt_off[i] = a.pt_off[i];
     }
-    if (pl.max_splits > kMaxCombineSplits) return hipErrorInvalidValue;
-
-    const dim3 grid(pl.max_splits, pl.units, a.nb);
-    hipError_t e;
-    switch (a.dtype) {
-        case QR_DTYPE_F32: e = dispatch_gmax<float>(gmax, k, grid, stream); break;
-        case QR_DTYPE_F16: e = dispatch_gmax<F16Tag>(gmax, k, grid, stream); break;
-        default: e = dispatch_gmax<BF16Tag>(gmax, k, grid, stream); break;
-    }
-    if (e != hipSuccess || pl.max_splits == 1) return e;
+    if (pl.max_splits > kMaxSplits) return hipErrorInvalidValue;
+    const void* fn = select_kernel(a.dtype, gmax, a.geom.head_dim);
+    void* args[] = {&k};
+    hipError_t e = hipLaunchKernel(fn, dim3(pl.max_splits, k.units, a.nb), dim3(kThreads), args, 0, stream);
+    if (e != hipSuccess) return e;
+    if (after_split && (e = hipEventRecord(after_split, stream)) != hipSuccess) return e;
+    if (pl.max_splits == 1) return hipSuccess;
     hipLaunchKernelGGL(decode_combine_kernel, dim3(a.heads, a.nb), dim3(kThreads), 0, stream, k);
     return hipGetLastError();
 }

@@ -79,8 +79,10 @@ struct DecodePlan {
     size_t workspace_bytes;
 };
 DecodePlan plan_decode(const DecodeArgs& a);
-// workspace: at least plan.workspace_bytes of device memory.
-hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, void* workspace,
-                         hipStream_t stream);
+// workspace: at least plan.workspace_bytes of device memory (split partials).
+// after_split: when not null, recorded on `stream` between the split kernel
+// and the combine kernel (benchmark instrumentation).
+hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, void* workspace, hipStream_t stream,
+                         hipEvent_t after_split = nullptr);
 
 }  // namespace qr

@@ -21,6 +21,7 @@ struct qr_kv {
     hipStream_t stream = nullptr;
     DevBuf stage;      // host <-> device staging of rows, queries and outputs
     DevBuf workspace;  // split-K partials
+    hipEvent_t split_event = nullptr;  // benchmark instrumentation (qr_kv_set_split_event)
 };
 
 namespace {
@@ -103,7 +104,7 @@ int decode_dev(qr_kv* kv, int n, const int* seq_ids, const int* seq_len, int lay
         }
         const DecodePlan plan = plan_decode(a);
         QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
-        QR_HIP(launch_decode(a, plan, kv->workspace.get(), stream));
+        QR_HIP(launch_decode(a, plan, kv->workspace.get(), stream, kv->split_event));
     }
     return QR_OK;
 }
@@ -360,6 +361,13 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
     QR_TRY(check_handle(kv));
     return chunk_common(kv, seq_id, layer, pos0, nq, q_dev, q_dtype, attn_dev, true, true, scale,
                         as_stream(stream));
+}
+
+int qr_kv_set_split_event(qr_kv* kv, void* event) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    kv->split_event = static_cast<hipEvent_t>(event);
+    return QR_OK;
 }
 
 int qr_kv_reset(qr_kv* kv, int seq_id) {

@@ -145,7 +145,8 @@ def test_batch_independent_page_tables(gpu):
             check_decode(out[s], data[s][0], data[s][1], q[s], heads, kv_heads, D, 0.088, f"batch seq {s}")
         # the same entry twice and out of order
         out2 = kv.AttentionBatch(1, [3, 0, 3], [lens[3] - 1, lens[0] - 1, 100], q[[3, 0, 1]], 0.088)
-        assert np.array_equal(out2[0], out[3]) and np.array_equal(out2[1], out[0])
+        assert_close(out2[0], out[3], 1e-6, 1e-5, "repeat entry 3")
+        assert_close(out2[1], out[0], 1e-6, 1e-5, "repeat entry 0")
         check_decode(out2[2], data[3][0][:101], data[3][1][:101], q[1], heads, kv_heads, D, 0.088, "batch pos 100")
 
 
@@ -265,8 +266,9 @@ def test_c2_llama8b_decode_32k_batch16_fp16(gpu):
             K, V = seqs[b]
             check_decode(out[b], K.astype(np.float32), V.astype(np.float32), q[b], heads, kv_heads, D,
                          1 / math.sqrt(D), f"C2 f16 B16 entry {b}")
-        for b in (3, 12):  # batching does not change an entry's bits
-            assert np.array_equal(kv.Attention(0, n - 1, q[b], 1 / math.sqrt(D), seq_id=b), out[b])
+        for b in (3, 12):  # a batched entry equals the same query alone (split sizes follow the batch)
+            assert_close(kv.Attention(0, n - 1, q[b], 1 / math.sqrt(D), seq_id=b), out[b], 1e-6, 1e-5,
+                         f"B16 entry {b} vs single")
 
 
 def test_c4_llama70b_decode_128k_fp16(gpu):
