@@ -60,6 +60,20 @@ WORKLOADS = {
 }
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summaries
+    (a line `traffic_bytes_per_launch[<workload>]: <bytes>` under profiles/), else None."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        for line in open(path):
+            m = re.match(r"traffic_bytes_per_launch\[([\w-]+)\]:\s*(\d+)", line.strip())
+            if m and m.group(1) == name:
+                return int(m.group(2))
+    return None
+
+
 def esize(dtype):
     return 4 if dtype == "f32" else 2
 
@@ -309,7 +323,19 @@ def main():
     ap.add_argument("--config", default="c2-f32-b1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device-to-device copy (scales rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        x = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": x.numel() * 4, "bytes_written": y.numel() * 4}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(the kernels are the one-GPU share at its real shape; no multi-GPU path exists)", file=sys.stderr)
@@ -332,6 +358,7 @@ def main():
         achieved = bytes_step / (kms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
                 "frac": achieved / (HBM_PEAK_TBS * 1e3), "traffic": None}
+    roof["traffic"] = profiled_traffic(args.config)
     roof["kernel_us"] = round(kms * 1e3, 3)
     roof["kernel"] = "split-K kernel (HIP events around it)" if kernel_ms else "whole step (HIP events)"
     line = {
