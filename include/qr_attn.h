@@ -148,7 +148,9 @@ int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, v
 
 /* ctor MlaLatentCache(layers, latentDim, maxSeq), MlaLatentCache.cs:22-27, with
  * latentDim = kv_lora + rope (StreamingEngine.cs:96).  dtype: F32, F16 or BF16.
- * kv_lora must be a multiple of 64 (<= 1024) and rope a multiple of 16 (<= 256). */
+ * 1 <= kv_lora <= 1024, 0 <= rope <= 256.  16-bit caches with kv_lora 512 and rope
+ * 0 or 64 run on MFMA tiles with fp16 operands (bf16 latents must lie in the fp16
+ * range, |x| < 65504); every other shape runs a generic fp32 kernel. */
 int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, int dtype);
 int qr_mla_destroy(qr_mla* mla);
 int qr_mla_reserve(qr_mla* mla, int pages);

@@ -108,10 +108,8 @@ int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, 
     QR_CHECK_ARG(out != nullptr, "null output handle pointer");
     *out = nullptr;
     QR_CHECK_ARG(layers >= 1, "layers must be >= 1 (got %d)", layers);
-    QR_CHECK_ARG(kv_lora >= 64 && kv_lora <= kMlaMaxLora && kv_lora % 64 == 0,
-                 "kv_lora %d unsupported (multiple of 64, <= %d)", kv_lora, kMlaMaxLora);
-    QR_CHECK_ARG(rope >= 0 && rope <= kMlaMaxRope && rope % 16 == 0,
-                 "rope %d unsupported (multiple of 16, <= %d)", rope, kMlaMaxRope);
+    QR_CHECK_ARG(kv_lora >= 1 && kv_lora <= kMlaMaxLora, "kv_lora %d outside [1, %d]", kv_lora, kMlaMaxLora);
+    QR_CHECK_ARG(rope >= 0 && rope <= kMlaMaxRope, "rope %d outside [0, %d]", rope, kMlaMaxRope);
     QR_CHECK_ARG(max_seq >= 1, "max_seq must be >= 1 (got %d)", max_seq);
     QR_CHECK_ARG(dtype_valid(dtype), "unknown dtype %d", dtype);
     qr_mla* m = new (std::nothrow) qr_mla();

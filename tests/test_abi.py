@@ -49,7 +49,8 @@ def test_kv_create_validates_before_device(args, needle):
     assert needle in L.qr_last_error().decode()
 
 
-@pytest.mark.parametrize("args", [(0, 512, 64, 100, 2), (1, 500, 64, 100, 2), (1, 512, 60, 100, 2), (1, 512, 64, 100, 9)])
+@pytest.mark.parametrize("args", [(0, 512, 64, 100, 2), (1, 0, 64, 100, 2), (1, 2048, 64, 100, 2), (1, 512, -1, 100, 2),
+                                  (1, 512, 64, 0, 2), (1, 512, 64, 100, 9)])
 def test_mla_create_validates_before_device(args):
     L = qr.load()
     h = ctypes.c_void_p()
