@@ -4,6 +4,7 @@
 #include <new>
 #include <vector>
 
+#include "qr_chunk.hpp"
 #include "qr_store.hpp"
 
 namespace qr {
@@ -337,9 +338,29 @@ int chunk_common(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void*
         qf = q32;
     }
     float* dout = out_is_dev ? attn : q32 + nq * rowf;
-    std::vector<int> ids(nq, seq_id), lens(nq);
-    for (int i = 0; i < nq; ++i) lens[i] = pos0 + i + 1;
-    QR_TRY(decode_dev(kv, nq, ids.data(), lens.data(), layer, qf, dout, scale, stream));
+    if (chunk_mfma_eligible(kv->dtype, kv->head_dim, kv->heads, kv->kv_heads)) {
+        // MFMA tiles read each K/V tile once for a block of queries
+        ChunkArgs c{};
+        c.pool = kv->store.pool();
+        c.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+        c.geom = kv->store.geom();
+        c.kv_dtype = kv->dtype;
+        c.heads = kv->heads;
+        c.pos0 = pos0;
+        c.nq = nq;
+        c.q = qsrc;
+        c.q_dtype = q_dtype;
+        c.out = dout;
+        c.scale = scale;
+        const ChunkPlan plan = plan_chunk(c);
+        QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+        QR_HIP(launch_chunk(c, plan, kv->workspace.get(), stream, kv->split_event));
+    } else {
+        // exact fp32 path: every query is one decode entry with its causal length
+        std::vector<int> ids(nq, seq_id), lens(nq);
+        for (int i = 0; i < nq; ++i) lens[i] = pos0 + i + 1;
+        QR_TRY(decode_dev(kv, nq, ids.data(), lens.data(), layer, qf, dout, scale, stream));
+    }
     if (!out_is_dev) {
         QR_HIP(hipMemcpyAsync(attn, dout, fbytes, hipMemcpyDeviceToHost, stream));
         QR_HIP(hipStreamSynchronize(stream));
