@@ -4,7 +4,7 @@
 // (StreamingEngine.cs:531-568).  Latent pages are token-major rows of
 // kv_lora + rope elements ([c_kv | k_pe], StreamingEngine.cs:494-506).
 //
-// mla_mfma_kernel (bf16/f16 latents, kv_lora 512, rope 0 or 64): MFMA tiles, see
+// mla_tile_kernel (bf16/f16 latents, kv_lora 512, rope 0 or 64): MFMA tiles, see
 //   below; splits merged by mla_combine_wide_kernel.
 // mla_split_generic_kernel: one workgroup per (split of 256 positions, head).
 //   Scores of the split are staged in LDS; the split's partial (max, sum,
@@ -143,276 +143,430 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // ---------------------------------------------------------------------------
 // MFMA path for 16-bit latents (kv_lora 512, rope 0 or 64).
 //
-// Workgroup = 4 waves = 64 heads (16 per wave) over one split of the sequence.
-// The split is walked in tiles of 32 positions; each tile is staged in LDS twice:
-// row-major [token][kv_lora+rope] (QK operand) and transposed [dim][token] over the
-// first kv_lora dims (PV operand), so every MFMA operand is one or two vector LDS
-// reads.  v_mfma_f32_16x16x32_{bf16,f16} lane layout (verified on gfx950):
+// Workgroup = 4 waves = 32 heads over one split of the sequence, walked in tiles
+// of 64 positions.  A tile (64 latent rows, contiguous inside one page) is copied
+// into LDS by the LDS-DMA path (global_load_lds_dwordx4), into one of two
+// buffers, so the copy of tile t+1 runs under the MFMAs of tile t.
+//   QK  wave w scores positions 16w..16w+15 of the tile for all 32 heads:
+//       S^T[pos][head] = C[pos][dims] . q~^T[dims][head]; A is read from the
+//       row-major tile, B = q~ (fp16) stays in registers.
+//   The scores go through LDS so that every wave sees all 64 positions; every
+//   wave runs the same online softmax (log2 units) and so holds the same (m, l).
+//   PV  wave w owns latent dims 128w..128w+127 for all 32 heads:
+//       U^T[dim][head] += C^T[dim][pos] . P^T[pos][head]; the C^T operand is read
+//       from the same row-major tile with ds_read_b64_tr_b16.
+// v_mfma_f32_16x16x32_f16 lane layout (checked on gfx950):
 //   A[m = lane%16][k = 8*(lane/16)+i], B[k = 8*(lane/16)+i][n = lane%16],
 //   D[m = 4*(lane/16)+r][n = lane%16].
-//   QK: S^T[token][head] = C[token][dims] . q~^T[dims][head]      (M tokens, N heads)
-//   PV: U^T[dim][head]  += C^T[dim][tokens] . P^T[tokens][head]    (M dims,   N heads)
-// In PV the 8 k-slots of lane quarter q are tokens {4q..4q+3, 16+4q..16+4q+3}: exactly
-// the 8 scores that lane holds after QK, so P goes from the QK result straight into
-// the B operand.  Each lane owns one head (lane%16) in both results, so the online
-// softmax rescale of its U tiles is lane-local.
-// Operands are fp16 for both 16-bit cache types: bf16 latents are widened to fp16
-// while the tile is staged (exact for |x| in the fp16 range, 2^-24..65504), which
-// keeps 11 mantissa bits for q~ and P instead of bf16's 8.  q~ is pre-multiplied per
-// head by a power of two that brings its largest element to at most 2^14 (exact) and
-// the scores are scaled back, so q~ never overflows fp16.
-constexpr int kTileTok = 32;
+// ds_read_b64_tr_b16 (checked on gfx950): inside each group of 16 lanes, lane j
+//   receives element i (0..3) from the 8 bytes addressed by lane 4i + j/4, at
+//   element j%4 of them.
+// In PV the 8 k-slots of lane quarter q are the positions {4q..4q+3, 16+4q..16+4q+3}
+// of a 32-position step, so each half of a transposed read touches 8 distinct rows.
+// QK runs in fp16 for both cache types: q~ keeps 11 mantissa bits (bf16's 8 would
+// dominate the error), bf16 latent elements are converted when read from LDS
+// (exact for |x| in the fp16 normal range).  q~ is pre-multiplied per head by the
+// power of two that brings its largest element to at most 2^14 (exact) and the
+// scores are scaled back, so q~ never overflows fp16.  PV runs in the cache's type:
+// the latent is used unconverted and P (in [0, 1]) is rounded to fp16 or bf16.
+// LDS tile layout: blocks of 8 logical 16-byte chunks (128 bytes) x 64 rows; inside
+// a block, chunk c of row r sits at slot (c % 8) ^ f(r), where f(r) is the 3-bit
+// reversal of (r >> 1) & 7, so the 16 rows of a QK read and the 8 rows of half a
+// transposed read fall on distinct banks.
+constexpr int kMTile = 64;                 // positions per tile
+constexpr int kMHeads = 32;                // heads per workgroup
 constexpr int kMfmaLora = 512;
-constexpr int kMfmaHeads = 64;  // per workgroup
+constexpr int kScoreStride = kMTile + 4;   // floats per head row of the score buffer
+constexpr float kRescaleSlack = 8.f;       // log2 units
+constexpr int kBufferFlags = 0x00020000;   // raw buffer resource word 3 (gfx9 family)
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_ptr;
 
-template <typename T> struct Mfma16;
-template <> struct Mfma16<__bf16> {
-    using vec = bf16x8_t;
-    __device__ static f32x4_t mma(vec a, vec b, f32x4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-    __device__ static __bf16 from_f32(float x) { return static_cast<__bf16>(x); }  // round to nearest even
-    __device__ static float to_f32(__bf16 x) { return static_cast<float>(x); }
-};
-template <> struct Mfma16<_Float16> {
-    using vec = f16x8_t;
+__device__ __forceinline__ int row_swizzle(int r) {
+    const int x = (r >> 1) & 7;
+    return ((x & 1) << 2) | (x & 2) | (x >> 2);
+}
+
+// Two packed bf16 -> two packed fp16 (v_cvt_pk_f16_f32: exact in the fp16 normal range).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t f = {__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
+}
+
+// QK operand from 16 cache bytes: fp16 as is, bf16 converted to fp16.
+template <bool SRC_BF16>
+__device__ __forceinline__ f16x8_t qk_operand(const U32x4& r) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = SRC_BF16 ? u32x4_t{bf16x2_to_f16x2(r.x), bf16x2_to_f16x2(r.y), bf16x2_to_f16x2(r.z), bf16x2_to_f16x2(r.w)}
+                               : u32x4_t{r.x, r.y, r.z, r.w};
+    return __builtin_bit_cast(f16x8_t, v);
+}
+
+// PV runs in the cache's own 16-bit type: the latent goes to the MFMA unconverted
+// and P is rounded to that type (P is in [0, 1]).
+template <bool SRC_BF16> struct PvType;
+template <> struct PvType<false> {
+    typedef _Float16 elem;
+    typedef f16x8_t vec;
     __device__ static f32x4_t mma(vec a, vec b, f32x4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-    __device__ static _Float16 from_f32(float x) { return static_cast<_Float16>(x); }
-    __device__ static float to_f32(_Float16 x) { return static_cast<float>(x); }
 };
+template <> struct PvType<true> {
+    typedef __bf16 elem;
+    typedef __bf16 vec __attribute__((ext_vector_type(8)));
+    __device__ static f32x4_t mma(vec a, vec b, f32x4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+
+// Workgroup barrier ordering LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// Workgroup barrier for data written with ds_write while an LDS-DMA is in flight:
+// it waits for this wave's LDS instructions (lgkmcnt) only.  A release fence
+// would also wait for the DMA (its LDS writes count as vector-memory loads).
+__device__ __forceinline__ void lds_barrier_dma_in_flight() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// s_waitcnt vmcnt(0): this wave's LDS-DMA writes have landed.
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
+// ... lds).  Written as inline asm so that the compiler, which cannot tell the LDS
+// range a DMA writes, does not insert waits for it before unrelated LDS reads;
+// completion is awaited explicitly with wait_dma() before the data is read.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, const char* lds, uint32_t voffset,
+                                                  uint32_t soffset) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)lds)));
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
+}
 
 struct MlaMK {
     const char* pool;
     const int* page_table;
     int heads;
     int seq_len;
-    int split_tokens;
+    int split_tokens;  // multiple of kMTile
     int splits;
+    int groups;        // head groups of kMHeads
+    int per_xcd;       // launch slots per XCD
     const float* q_tilde;
     const float* q_rope;
     float* u;
-    float* part_u;     // [heads][splits][kv_lora]
-    float2* part_ml;   // [heads][splits]
+    void* part_u;      // [heads][splits][kv_lora] fp16, normalised by l
+    float2* part_ml;   // [heads][splits] (m, l)
     float qscale;      // scale * log2(e)
 };
 
 template <bool SRC_BF16, int KR>
-__global__ void __launch_bounds__(256) mla_mfma_kernel(const MlaMK p) {
-    using T = _Float16;
-    using M = Mfma16<T>;
-    using V = typename M::vec;
+__global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     constexpr int KL = kMfmaLora;
-    constexpr int W = KL + KR;             // latent width
-    constexpr int NK = W / 32;              // QK k-steps
-    constexpr int NT = KL / 16;             // PV dim tiles
-    constexpr int RS = W * 2 + 16;          // row-major LDS row stride (bytes), padded
-    constexpr int TS = kTileTok * 2 + 8;    // transposed LDS row stride (bytes), padded
-    constexpr int CHUNKS = kTileTok * W / 8; // 16-byte chunks per tile
-    constexpr int CPT = (CHUNKS + 255) / 256;
+    constexpr int W = KL + KR;            // latent width (elements)
+    constexpr int RB = W * 2;             // row bytes
+    constexpr int CR = W / 8;             // 16-byte chunks per row
+    constexpr int NK = W / 32;            // QK k-steps
+    constexpr int TB = kMTile * RB;       // tile bytes = CR KiB
+    constexpr int DMA_PER_WAVE = CR / 4;  // 1 KiB DMA instructions per wave per tile
+    constexpr int QS = RB + 16;           // row stride of the staged q~ (bytes)
+    static_assert(kMHeads * QS <= TB, "q~ staging must fit in one tile buffer");
 
-    __shared__ __attribute__((aligned(16))) char lds_rm[kTileTok * RS];
-    __shared__ __attribute__((aligned(16))) char lds_tr[KL * TS];
+    __shared__ __attribute__((aligned(1024))) char lds_t0[TB];
+    __shared__ __attribute__((aligned(1024))) char lds_t1[TB];
+    __shared__ __attribute__((aligned(16))) float lds_s[kMHeads * kScoreStride];
+    __shared__ int lds_qexp[kMHeads];
 
-    const int split = blockIdx.x;
-    const int hg = blockIdx.y;
+    // Launch slot b runs on XCD b % 8; consecutive logical indices (the head groups
+    // of one split, then the next split) are kept on one XCD so its L2 serves the
+    // repeated reads of a split's latent rows.
+    const int b = blockIdx.x;
+    const int idx = (b & 7) * p.per_xcd + (b >> 3);
+    if (idx >= p.groups * p.splits) return;
+    const int hg = idx % p.groups;
+    const int split = idx / p.groups;
     const int t_begin = split * p.split_tokens;
     const int t_end = min(p.seq_len, t_begin + p.split_tokens);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int q4 = lane >> 4;                // lane quarter
-    const int hl = lane & 15;
-    const int head = hg * kMfmaHeads + wave * 16 + hl;
-    const int hq = min(head, p.heads - 1);
+    const int ntiles = (t_end - t_begin + kMTile - 1) / kMTile;  // >= 1
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;  // wave-uniform (SGPR), 0..3
+    const int q4 = lane >> 4;
+    const int l16 = lane & 15;
 
-    // ---- q~ (and q_rope) as B operands: lane holds dims 32*kk + 8*q4 .. +8 of head hl,
-    // scaled by 2^-e so the head's largest |element| is at most 2^14
-    float qf[NK][8];
-    float amax = 0.f;
+    // LDS-DMA of the tile at t0 into buffer `dst`: instruction n fills bytes
+    // [1024n, 1024n + 1024), lane j the 16 bytes at 1024n + 16j, i.e. slot P = 64n + j
+    // = row P / CR, swizzled chunk P % CR.  Rows past the sequence end repeat the
+    // last valid row (finite data under a zero weight).
+    // Buffer-load DMA of one tile.  Block g of the LDS tile (8 KiB) holds logical
+    // chunks 8g..8g+7 of all 64 rows, 128 bytes per row; instruction (g, j) fills
+    // rows 8j..8j+7 of block g, lane L the row 8j + L/8, slot L%8, which holds chunk
+    // 8g + ((L%8) ^ f(row)).  Rows past the sequence end are outside the buffer
+    // range and read as zeros.
+    const int drow = lane >> 3;
+    int dma_voff[2];  // per parity of j: f(8j + L/8) = rev3(4 (j & 1) + L/16)
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
+    for (int jp = 0; jp < 2; ++jp) {
+        const int x = 4 * jp + (lane >> 4);
+        const int f = ((x & 1) << 2) | (x & 2) | (x >> 2);
+        dma_voff[jp] = drow * RB + 16 * ((lane & 7) ^ f);
+    }
+    auto dma = [&](int t0, long long phys, char* dst) {
+        const char* base = p.pool + (phys * kPageTokens + (t0 & (kPageTokens - 1))) * RB;
+        const int bytes = min(kMTile, t_end - t0) * RB;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, bytes, kBufferFlags);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int d = 32 * kk + 8 * q4 + i;
-            const float x = d < KL ? p.q_tilde[static_cast<size_t>(hq) * KL + d]
-                                   : p.q_rope[static_cast<size_t>(hq) * KR + (d - KL)];
-            qf[kk][i] = x;
-            amax = fmaxf(amax, fabsf(x));
-        }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    int qexp = 0;
-    if (amax > 16384.f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
-    const float qdown = ldexpf(1.f, -qexp);
-    const float sscale = p.qscale * ldexpf(1.f, qexp);  // score scale, undoing the q~ scaling
-    V qv[NK];
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qv[kk][i] = M::from_f32(qf[kk][i] * qdown);
-
-    f32x4_t acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.f;
-
-    // ---- staging of one tile: thread loads CPT 16-byte chunks
-    auto load_tile = [&](int t0, U32x4 (&r)[CPT]) {
-        const long long phys = p.page_table[t0 >> kPageShift];
-        const char* base = p.pool + (phys * kPageTokens + (t0 & (kPageTokens - 1))) * W * 2;
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int gi = c * 256 + threadIdx.x;
-            if (gi < CHUNKS) {
-                const int tok = gi / (W / 8);
-                const int col = gi - tok * (W / 8);
-                r[c] = (t0 + tok < t_end) ? load16(base + static_cast<long long>(tok) * W * 2 + col * 16)
-                                          : U32x4{0u, 0u, 0u, 0u};
-            }
+        for (int i = 0; i < DMA_PER_WAVE; ++i) {
+            const int n = wave + 4 * i;  // wave-uniform
+            const int g = n >> 3, j = n & 7;
+            buffer_load_lds16(rsrc, dst + 8192 * g + 1024 * j, dma_voff[j & 1], 8 * j * RB + 128 * g);
         }
     };
-    auto store_tile = [&](const U32x4 (&r)[CPT]) {
+    dma(t_begin, p.page_table[t_begin >> kPageShift], lds_t0);
+    // page of the next tile to copy, loaded one tile ahead
+    int phys_next = ntiles > 1 ? p.page_table[(t_begin + kMTile) >> kPageShift] : 0;
+
+    // ---- q~ of the 32 heads: fp32 -> fp16 scaled by 2^-qexp, staged in buffer 1.
+    // Eight consecutive threads share a head; thread `part` takes float4 columns
+    // part, part + 8, ...
+    {
+        const int hl = tid >> 3;
+        const int part = tid & 7;
+        const int head = min(hg * kMHeads + hl, p.heads - 1);
+        float4 v[NK];
+        float amax = 0.f;
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int gi = c * 256 + threadIdx.x;
-            if (gi < CHUNKS) {
-                const int tok = gi / (W / 8);
-                const int col = gi - tok * (W / 8);
-                U32x4 v = r[c];
-                if (SRC_BF16) {  // widen bf16 -> fp32 -> fp16 (exact inside the fp16 range)
-                    uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const _Float16 lo = static_cast<_Float16>(__uint_as_float(w4[i] << 16));
-                        const _Float16 hi = static_cast<_Float16>(__uint_as_float(w4[i] & 0xFFFF0000u));
-                        w4[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-                                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
-                    }
-                    v = U32x4{w4[0], w4[1], w4[2], w4[3]};
-                }
-                *reinterpret_cast<U32x4*>(lds_rm + tok * RS + col * 16) = v;
-                if (col * 8 < KL) {
-                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const uint16_t e = static_cast<uint16_t>(w4[i >> 1] >> ((i & 1) * 16));
-                        *reinterpret_cast<uint16_t*>(lds_tr + (col * 8 + i) * TS + tok * 2) = e;
-                    }
-                }
-            }
+        for (int i = 0; i < NK; ++i) {
+            const int d = 4 * (part + 8 * i);
+            v[i] = d < KL ? *reinterpret_cast<const float4*>(p.q_tilde + static_cast<size_t>(head) * KL + d)
+                          : *reinterpret_cast<const float4*>(p.q_rope + static_cast<size_t>(head) * KR + (d - KL));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         }
+        amax = fmaxf(amax, dpp_xor1(amax));
+        amax = fmaxf(amax, dpp_xor2(amax));
+        amax = fmaxf(amax, dpp_half_mirror(amax));
+        int qexp = 0;
+        if (amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
+        const float down = ldexpf(1.f, -qexp);
+#pragma unroll
+        for (int i = 0; i < NK; ++i) {
+            const _Float16 h0 = static_cast<_Float16>(v[i].x * down), h1 = static_cast<_Float16>(v[i].y * down);
+            const _Float16 h2 = static_cast<_Float16>(v[i].z * down), h3 = static_cast<_Float16>(v[i].w * down);
+            const uint2 w2 = make_uint2(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16),
+                                        static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h2)) |
+                                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h3)) << 16));
+            *reinterpret_cast<uint2*>(lds_t1 + hl * QS + 8 * (part + 8 * i)) = w2;
+        }
+        if (part == 0) lds_qexp[hl] = qexp;
+    }
+    lds_barrier();
+    // B operands of QK: head 16nt + l16, dims 32kk + 8q4 .. +8
+    f16x8_t qv[2][NK];
+    float sscale[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int hr = 16 * nt + l16;
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk)
+            qv[nt][kk] = *reinterpret_cast<const f16x8_t*>(lds_t1 + hr * QS + 64 * kk + 16 * q4);
+        sscale[nt] = p.qscale * ldexpf(1.f, lds_qexp[hr]);
+    }
+
+    // Per-lane LDS offsets (layout of the DMA above).  QK: row 16w + l16, logical
+    // chunk 4kk + q4 = block kk/2, slot 4 (kk & 1) + q4, stored at slot
+    // (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) + (q4 ^ (f & 3)).
+    const int rq = 16 * wave + l16;
+    const int fq = row_swizzle(rq);
+    const int qk_off = rq * 128 + 16 * (q4 ^ (fq & 3));
+    const int qk_flip = fq >> 2;
+    // PV: half h of the A operand of dim tile dt, step ks reads row
+    // 32ks + 16h + 4q4 + l16/4, dims 128w + 16dt + 4(l16 & 3) .. +4: logical chunk
+    // 16w + 2dt + ((l16 & 3) >> 1) = block 2w + dt/4, slot 2 (dt & 3) + ((l16 & 3) >> 1),
+    // byte 8 (l16 & 1).  f of that row depends on 4q4 + l16/4 only.
+    const int rp = 4 * q4 + (l16 >> 2);
+    const int fp = row_swizzle(rp);
+    const int a4 = l16 & 3;
+    const int pv_off = 16384 * wave + rp * 128 + 16 * ((a4 >> 1) ^ (fp & 1)) + 8 * (a4 & 1);
+    int pv_dt[4];  // slot pair of dt & 3: 2 ((dt & 3) ^ (f >> 1)) chunks
+#pragma unroll
+    for (int x = 0; x < 4; ++x) pv_dt[x] = 32 * (x ^ (fp >> 1));
+
+    f32x4_t acc[2][8];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[nt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {-INFINITY, -INFINITY};
+    float l[2] = {0.f, 0.f};
+
+    // One tile; `tile` and `next` are always the two distinct buffers by name, so
+    // the compiler can tell the LDS reads of `tile` from the DMA into `next` and
+    // does not wait for that DMA before reading.
+    auto step = [&](int it, const char* tile, char* next) __attribute__((always_inline)) {
+        const int t0 = t_begin + it * kMTile;
+        wait_dma();
+        lds_barrier();  // tile `it` is in LDS; tile it-1 and its scores are consumed
+        if (it + 1 < ntiles) dma(t0 + kMTile, __builtin_amdgcn_readfirstlane(phys_next), next);
+        if (it + 2 < ntiles) phys_next = p.page_table[(t0 + 2 * kMTile) >> kPageShift];
+
+        // ---- QK
+        f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+            const U32x4 raw = *reinterpret_cast<const U32x4*>(tile + 8192 * (kk >> 1) + qk_off + 64 * ((kk & 1) ^ qk_flip));
+            const f16x8_t av = qk_operand<SRC_BF16>(raw);
+            sc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qv[0][kk], sc[0], 0, 0, 0);
+            sc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qv[1][kk], sc[1], 0, 0, 0);
+        }
+        // lane holds positions 16w + 4q4 + r of heads 16nt + l16
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            float4 s4;
+            const int pos = t0 + 16 * wave + 4 * q4;
+            s4.x = pos + 0 < t_end ? sc[nt][0] * sscale[nt] : -INFINITY;
+            s4.y = pos + 1 < t_end ? sc[nt][1] * sscale[nt] : -INFINITY;
+            s4.z = pos + 2 < t_end ? sc[nt][2] * sscale[nt] : -INFINITY;
+            s4.w = pos + 3 < t_end ? sc[nt][3] * sscale[nt] : -INFINITY;
+            *reinterpret_cast<float4*>(lds_s + (16 * nt + l16) * kScoreStride + 16 * wave + 4 * q4) = s4;
+        }
+        lds_barrier_dma_in_flight();
+
+        // ---- softmax over the 64 positions; P^T operands: k-slot 8q4 + i of step ks
+        // is position 32ks + 4q4 + i (i < 4) or 32ks + 16 + 4q4 + i - 4
+        using PV = PvType<SRC_BF16>;
+        typename PV::vec pb[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            float s[2][8];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const float* row = lds_s + (16 * nt + l16) * kScoreStride + 32 * ks + 4 * q4;
+                const float4 x = *reinterpret_cast<const float4*>(row);
+                const float4 y = *reinterpret_cast<const float4*>(row + 16);
+                s[ks][0] = x.x; s[ks][1] = x.y; s[ks][2] = x.z; s[ks][3] = x.w;
+                s[ks][4] = y.x; s[ks][5] = y.y; s[ks][6] = y.z; s[ks][7] = y.w;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) tmax = fmaxf(tmax, s[ks][i]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            // Lazy rescale: the reference m moves only when the tile max exceeds it by
+            // more than 2^8, so P = 2^(s - m) <= 256 and the accumulators are rescaled
+            // in few tiles (skipped by the whole wave when no lane needs it).
+            const bool grow = tmax > m[nt] + kRescaleSlack;
+            const bool rescale = grow && m[nt] != -INFINITY;
+            if (__builtin_amdgcn_ballot_w64(rescale)) {
+                const float corr = rescale ? fast_exp2(m[nt] - tmax) : 1.f;
+                l[nt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) acc[nt][dt] *= corr;
+            }
+            if (grow) m[nt] = tmax;
+            const float mref = m[nt] == -INFINITY ? 0.f : m[nt];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float e = fast_exp2(s[ks][i] - mref);
+                    l[nt] += e;
+                    pb[nt][ks][i] = static_cast<typename PV::elem>(e);
+                }
+        }
+
+        // ---- PV over this wave's 128 dims
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const char* a0 = tile + pv_off + 8192 * (dt >> 2) + 4096 * ks + pv_dt[dt & 3];
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4_ptr)(a0));
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4_ptr)(a0 + 2048));
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                const u32x2_t lw = __builtin_bit_cast(u32x2_t, lo);
+                const u32x2_t hw = __builtin_bit_cast(u32x2_t, hi);
+                typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                const auto av = __builtin_bit_cast(typename PV::vec, u32x4_t{lw.x, lw.y, hw.x, hw.y});
+                acc[0][dt] = PV::mma(av, pb[0][ks], acc[0][dt]);
+                acc[1][dt] = PV::mma(av, pb[1][ks], acc[1][dt]);
+            }
     };
-
-    const int ntiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    U32x4 stage[CPT];
-    load_tile(t_begin, stage);
-    for (int it = 0; it < ntiles; ++it) {
-        const int t0 = t_begin + it * kTileTok;
-        __syncthreads();  // previous tile's readers are done
-        store_tile(stage);
-        __syncthreads();
-        if (it + 1 < ntiles) load_tile(t0 + kTileTok, stage);  // in flight during the MFMAs
-
-        // QK: two 16-token M tiles
-        f32x4_t sc[2];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            sc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            const char* row = lds_rm + (16 * mt + hl) * RS + 8 * q4 * 2;
-#pragma unroll
-            for (int kk = 0; kk < NK; ++kk) {
-                const V a = *reinterpret_cast<const V*>(row + 64 * kk);
-                sc[mt] = M::mma(a, qv[kk], sc[mt]);
-            }
-        }
-        // online softmax for head hl over this tile's 32 tokens
-        float s[8];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = t0 + 16 * mt + 4 * q4 + r;
-                const float v = tok < t_end ? sc[mt][r] * sscale : -INFINITY;
-                s[4 * mt + r] = v;
-                tmax = fmaxf(tmax, v);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        if (tmax > m) {
-            const float corr = m == -INFINITY ? 0.f : fast_exp2(m - tmax);
-            l *= corr;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] *= corr;
-            m = tmax;
-        }
-        const float mref = m == -INFINITY ? 0.f : m;
-        V pb;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float e = fast_exp2(s[i] - mref);
-            l += e;
-            pb[i] = M::from_f32(e);
-        }
-        // PV: one 32-token k step per 16-dim tile
-        const char* col = lds_tr + hl * TS + 4 * q4 * 2;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const char* rp = col + 16 * t * TS;
-            const uint2 lo = *reinterpret_cast<const uint2*>(rp);
-            const uint2 hi = *reinterpret_cast<const uint2*>(rp + 32);
-            V a;
-            const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                a[i] = __builtin_bit_cast(T, static_cast<uint16_t>(w4[i >> 1] >> ((i & 1) * 16)));
-            acc[t] = M::mma(a, pb, acc[t]);
-        }
+    for (int it = 0; it < ntiles; it += 2) {
+        step(it, lds_t0, lds_t1);
+        if (it + 1 >= ntiles) break;
+        step(it + 1, lds_t1, lds_t0);
     }
 
-    // l: sum over the four lane quarters that share the head
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (head >= p.heads) return;
-    if (p.splits == 1) {
-        float* out = p.u + static_cast<size_t>(head) * KL;
-        const float inv = 1.f / l;
+    // l: sum over the four lane quarters that share a head
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float4 v = make_float4(acc[t][0] * inv, acc[t][1] * inv, acc[t][2] * inv, acc[t][3] * inv);
-            *reinterpret_cast<float4*>(out + 16 * t + 4 * q4) = v;
-        }
-        return;
+    for (int nt = 0; nt < 2; ++nt) {
+        l[nt] += __shfl_xor(l[nt], 16);
+        l[nt] += __shfl_xor(l[nt], 32);
     }
-    const size_t slot = static_cast<size_t>(head) * p.splits + split;
-    float* out = p.part_u + slot * KL;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-        *reinterpret_cast<float4*>(out + 16 * t + 4 * q4) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
-    if (q4 == 0) p.part_ml[slot] = make_float2(m, l);
+    for (int nt = 0; nt < 2; ++nt) {
+        const int head = hg * kMHeads + 16 * nt + l16;
+        if (head >= p.heads) continue;
+        const int dim0 = 128 * wave + 4 * q4;
+        if (p.splits == 1) {
+            float* out = p.u + static_cast<size_t>(head) * KL + dim0;
+            const float inv = 1.f / l[nt];
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt)
+                *reinterpret_cast<float4*>(out + 16 * dt) =
+                    make_float4(acc[nt][dt][0] * inv, acc[nt][dt][1] * inv, acc[nt][dt][2] * inv, acc[nt][dt][3] * inv);
+        } else {
+            // normalised split result u_s = acc / l in fp16 (a convex combination of
+            // latent rows, so inside the fp16 range the QK operands already need)
+            const size_t slot = static_cast<size_t>(head) * p.splits + split;
+            _Float16* out = static_cast<_Float16*>(p.part_u) + slot * KL + dim0;
+            const float inv = 1.f / l[nt];
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                typedef float f32x2_t __attribute__((ext_vector_type(2)));
+                typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+                const f16x2_t lo = __builtin_convertvector(f32x2_t{acc[nt][dt][0] * inv, acc[nt][dt][1] * inv}, f16x2_t);
+                const f16x2_t hi = __builtin_convertvector(f32x2_t{acc[nt][dt][2] * inv, acc[nt][dt][3] * inv}, f16x2_t);
+                *reinterpret_cast<uint2*>(out + 16 * dt) =
+                    make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+            }
+            if (wave == 0 && q4 == 0) p.part_ml[slot] = make_float2(m[nt], l[nt]);
+        }
+    }
 }
 
 // Split merge for the MFMA path: one workgroup per (head, 128-dim block); a thread
-// owns one float4 column and every 8th split, loading 8 partials at a time.
+// owns 4 dims of the block and every 8th split, loading 8 normalised fp16 partials
+// at a time; split s weighs l_s 2^(m_s - M).
 __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
     constexpr int KL = kMfmaLora;
     const int h = blockIdx.x;
     const int blk = blockIdx.y;             // 128-dim block
-    const int c4 = threadIdx.x & 31;        // float4 column inside the block
+    const int c4 = threadIdx.x & 31;        // 4-dim column inside the block
     const int grp = threadIdx.x >> 5;       // 8 split groups
     const size_t base = static_cast<size_t>(h) * p.splits;
     const int d = blk * 128 + c4 * 4;
+    const _Float16* part = static_cast<const _Float16*>(p.part_u);
     float m = -INFINITY, l = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = grp; s0 < p.splits; s0 += 64) {
-        float4 a[8];
+        uint2 a[8];
         float2 ml[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int s = s0 + 8 * i;
             const bool in = s < p.splits;
-            a[i] = in ? *reinterpret_cast<const float4*>(p.part_u + (base + s) * KL + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+            a[i] = in ? *reinterpret_cast<const uint2*>(part + (base + s) * KL + d) : make_uint2(0u, 0u);
             ml[i] = in ? p.part_ml[base + s] : make_float2(-INFINITY, 0.f);
         }
         float mb = m;
@@ -423,12 +577,15 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
         o.x *= cm; o.y *= cm; o.z *= cm; o.w *= cm;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float c = ml[i].x == -INFINITY ? 0.f : fast_exp2(ml[i].x - mb);
-            l = fmaf(ml[i].y, c, l);
-            o.x = fmaf(a[i].x, c, o.x);
-            o.y = fmaf(a[i].y, c, o.y);
-            o.z = fmaf(a[i].z, c, o.z);
-            o.w = fmaf(a[i].w, c, o.w);
+            const float w = ml[i].x == -INFINITY ? 0.f : ml[i].y * fast_exp2(ml[i].x - mb);
+            typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+            const f16x2_t lo = __builtin_bit_cast(f16x2_t, a[i].x);
+            const f16x2_t hi = __builtin_bit_cast(f16x2_t, a[i].y);
+            l += w;
+            o.x = fmaf(static_cast<float>(lo[0]), w, o.x);
+            o.y = fmaf(static_cast<float>(lo[1]), w, o.y);
+            o.z = fmaf(static_cast<float>(hi[0]), w, o.z);
+            o.w = fmaf(static_cast<float>(hi[1]), w, o.w);
         }
         m = mb;
     }
@@ -473,32 +630,37 @@ int cus() {
     return n;
 }
 
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
 }  // namespace
 
 MlaPlan plan_mla(const MlaArgs& a) {
     MlaPlan pl{};
+    size_t q_copy = 0;
     if (mfma_eligible(a)) {
-        // about one workgroup per CU: (64-head group) x split, splits of whole 32-token tiles
-        const int groups = (a.heads + kMfmaHeads - 1) / kMfmaHeads;
-        const int tiles = (a.seq_len + kTileTok - 1) / kTileTok;
+        // about one workgroup per CU: (32-head group) x split, splits of whole 64-position tiles
+        const int groups = (a.heads + kMHeads - 1) / kMHeads;
+        const int tiles = (a.seq_len + kMTile - 1) / kMTile;
         int want = std::max(1, cus() / groups);
         want = std::min(want, tiles);
         const int tiles_per_split = (tiles + want - 1) / want;
-        pl.split_tokens = tiles_per_split * kTileTok;
+        pl.split_tokens = tiles_per_split * kMTile;
+        // room for 16-byte aligned copies of q~ / q_rope when the caller's are not
+        q_copy = align256(static_cast<size_t>(a.heads) * a.kv_lora * 4) + align256(static_cast<size_t>(a.heads) * a.rope * 4);
     } else {
         pl.split_tokens = kGenericSplit;
     }
     pl.splits = (a.seq_len + pl.split_tokens - 1) / pl.split_tokens;
-    pl.workspace_bytes = pl.splits > 1
-        ? static_cast<size_t>(a.heads) * pl.splits * (static_cast<size_t>(a.kv_lora) * 4 + 8)
-        : 0;
+    const size_t slots = static_cast<size_t>(a.heads) * pl.splits;
+    const size_t part_elem = mfma_eligible(a) ? 2 : 4;  // fp16 partials on the MFMA path
+    pl.workspace_bytes = (pl.splits > 1 ? align256(slots * a.kv_lora * part_elem) + align256(slots * 8) : 0) + q_copy;
     return pl;
 }
 
 namespace {
 template <bool SRC_BF16, int KR>
-hipError_t launch_mfma(const MlaMK& k, int groups, hipStream_t stream) {
-    hipLaunchKernelGGL((mla_mfma_kernel<SRC_BF16, KR>), dim3(k.splits, groups), dim3(256), 0, stream, k);
+hipError_t launch_tile(const MlaMK& k, hipStream_t stream) {
+    hipLaunchKernelGGL((mla_tile_kernel<SRC_BF16, KR>), dim3(8 * k.per_xcd), dim3(256), 0, stream, k);
     return hipGetLastError();
 }
 }  // namespace
@@ -506,6 +668,7 @@ hipError_t launch_mfma(const MlaMK& k, int groups, hipStream_t stream) {
 hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipStream_t stream) {
     if (pl.splits > 4096) return hipErrorInvalidValue;
     const size_t slots = static_cast<size_t>(a.heads) * pl.splits;
+    char* ws = static_cast<char*>(workspace);
     if (mfma_eligible(a)) {
         MlaMK k{};
         k.pool = static_cast<const char*>(a.pool);
@@ -514,17 +677,31 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
         k.seq_len = a.seq_len;
         k.split_tokens = pl.split_tokens;
         k.splits = pl.splits;
+        k.groups = (a.heads + kMHeads - 1) / kMHeads;
+        k.per_xcd = (k.groups * pl.splits + 7) / 8;
+        k.u = a.u;
+        const size_t part_bytes = pl.splits > 1 ? align256(slots * a.kv_lora * 2) + align256(slots * 8) : 0;
+        k.part_u = ws;
+        k.part_ml = reinterpret_cast<float2*>(ws + align256(slots * a.kv_lora * 2));
+        // the kernel reads q~ / q_rope as float4
         k.q_tilde = a.q_tilde;
         k.q_rope = a.q_rope;
-        k.u = a.u;
-        k.part_u = static_cast<float*>(workspace);
-        k.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + slots * a.kv_lora * 4);
+        const bool misaligned = (reinterpret_cast<uintptr_t>(a.q_tilde) | reinterpret_cast<uintptr_t>(a.q_rope)) & 15;
+        if (misaligned) {
+            float* qt = reinterpret_cast<float*>(ws + part_bytes);
+            float* qr = reinterpret_cast<float*>(ws + part_bytes + align256(static_cast<size_t>(a.heads) * a.kv_lora * 4));
+            hipError_t e = hipMemcpyAsync(qt, a.q_tilde, static_cast<size_t>(a.heads) * a.kv_lora * 4, hipMemcpyDeviceToDevice, stream);
+            if (e == hipSuccess && a.rope)
+                e = hipMemcpyAsync(qr, a.q_rope, static_cast<size_t>(a.heads) * a.rope * 4, hipMemcpyDeviceToDevice, stream);
+            if (e != hipSuccess) return e;
+            k.q_tilde = qt;
+            k.q_rope = a.rope ? qr : nullptr;
+        }
         k.qscale = static_cast<float>(static_cast<double>(a.scale) * 1.4426950408889634);
-        const int groups = (a.heads + kMfmaHeads - 1) / kMfmaHeads;
         hipError_t e;
         const bool bf = a.dtype == QR_DTYPE_BF16;
-        if (a.rope) e = bf ? launch_mfma<true, 64>(k, groups, stream) : launch_mfma<false, 64>(k, groups, stream);
-        else e = bf ? launch_mfma<true, 0>(k, groups, stream) : launch_mfma<false, 0>(k, groups, stream);
+        if (a.rope) e = bf ? launch_tile<true, 64>(k, stream) : launch_tile<false, 64>(k, stream);
+        else e = bf ? launch_tile<true, 0>(k, stream) : launch_tile<false, 0>(k, stream);
         if (e != hipSuccess || pl.splits == 1) return e;
         hipLaunchKernelGGL(mla_combine_wide_kernel, dim3(a.heads, kMfmaLora / 128), dim3(256), 0, stream, k);
         return hipGetLastError();
@@ -543,8 +720,8 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
     k.q_tilde = a.q_tilde;
     k.q_rope = a.q_rope;
     k.u = a.u;
-    k.part_u = static_cast<float*>(workspace);
-    k.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + slots * a.kv_lora * 4);
+    k.part_u = reinterpret_cast<float*>(ws);
+    k.part_ml = reinterpret_cast<float2*>(ws + align256(slots * a.kv_lora * 4));
     k.qscale = static_cast<float>(static_cast<double>(a.scale) * 1.4426950408889634);
     hipLaunchKernelGGL(mla_split_generic_kernel, dim3(pl.splits, a.heads), dim3(kThreads), 0, stream, k);
     hipError_t e = hipGetLastError();

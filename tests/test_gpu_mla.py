@@ -50,6 +50,9 @@ def test_c5_mla_absorbed_decode_16k_bf16(gpu):
     ("bf16", 64, 0, 700, None),       # NoPE latent (GLM-5.3-Flash style)
     ("f16", 16, 64, 777, 31),         # fewer positions than one tile
     ("bf16", 128, 64, 600, 0),        # one position: u = c_0 exactly up to fp16 rounding
+    ("bf16", 8, 64, 500, None),       # fewer heads than one 32-head group
+    ("f16", 33, 0, 1300, None),       # one head past a group boundary
+    ("bf16", 128, 64, 9000, 5000),    # mid-sequence position, rows past it resident
 ])
 def test_mla_mfma_shapes(gpu, dtype, heads, rope, n, pos):
     got, lat, qt, qrp, s = run_mla(dtype, heads, 512, rope, n, pos=pos, seed=n)
@@ -109,3 +112,43 @@ def test_mla_cache_state(gpu):
             m.Append(1, 0, np.zeros(kv_lora + rope + 1, np.float32))
         with pytest.raises(qr.QrInvalidArgument):
             m.AbsorbedAttention(1, 10, normal(1, (300, kv_lora)), normal(2, (300, rope)), 0.1)
+
+
+def test_mla_rows_past_pos_are_not_read_into_the_result(gpu):
+    """Rows after pos hold NaN; attention at pos sees rows 0..pos only (seq = pos + 1)."""
+    n, pos, heads = 700, 300, 64
+    lat = normal(77, (n, 576))
+    bits, latd = to_dtype_bits(lat, "bf16")
+    bits = bits.copy()
+    bits[pos + 1:] = 0x7FC0  # bf16 quiet NaN
+    qt, qrp = normal(78, (heads, 512)), normal(79, (heads, 64))
+    scale = 1 / math.sqrt(192)
+    with qr.MlaLatentCache(1, 512, 64, n, dtype="bf16") as m:
+        m.AppendRange(0, 0, bits, src_dtype="bf16")
+        got = m.AbsorbedAttention(0, pos, qt, qrp, scale)
+    assert np.isfinite(got).all()
+    check_mla(got, latd[:pos + 1], qt, qrp, 512, 64, scale, 5e-3, "NaN rows past pos")
+
+
+def test_mla_dev_entry_with_unaligned_queries(gpu):
+    """The device entry point accepts q~ / q_rope views that are not 16-byte aligned."""
+    import torch
+    n, heads = 1500, 40
+    lat = normal(81, (n, 576))
+    bits, latd = to_dtype_bits(lat, "bf16")
+    qt, qrp = normal(82, (heads, 512)), normal(83, (heads, 64))
+    scale = 1 / math.sqrt(192)
+    dev = torch.device("cuda")
+    qt_buf = torch.zeros(heads * 512 + 1, dtype=torch.float32, device=dev)
+    qr_buf = torch.zeros(heads * 64 + 3, dtype=torch.float32, device=dev)
+    qt_buf[1:] = torch.from_numpy(qt.ravel()).to(dev)
+    qr_buf[3:] = torch.from_numpy(qrp.ravel()).to(dev)
+    u = torch.empty(heads * 512, dtype=torch.float32, device=dev)
+    with qr.MlaLatentCache(1, 512, 64, n, dtype="bf16") as m:
+        m.AppendRange(0, 0, bits, src_dtype="bf16")
+        m.AbsorbedAttentionDev(0, n - 1, qt_buf[1:], qr_buf[3:], u, scale)
+        torch.cuda.synchronize()
+        aligned = m.AbsorbedAttention(0, n - 1, qt, qrp, scale)
+    got = u.cpu().numpy().reshape(heads, 512)
+    assert np.array_equal(got, aligned)
+    check_mla(got, latd, qt, qrp, 512, 64, scale, 5e-3, "unaligned q")
