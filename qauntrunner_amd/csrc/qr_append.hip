@@ -36,9 +36,7 @@ __device__ __forceinline__ void convert_store(void* dst, int dst_dtype, long lon
 __device__ __forceinline__ long long page_offset(const PageGeom& g, long long phys, int plane,
                                                  int slot, int col) {
     const int kvh = col / g.head_dim;
-    const int d = col - kvh * g.head_dim;
-    return phys * g.page_elems() + plane * g.plane_elems() +
-           (static_cast<long long>(kvh) * kPageTokens + slot) * g.head_dim + d;
+    return g.offset(phys, plane, kvh, slot, col - kvh * g.head_dim);
 }
 
 __global__ void __launch_bounds__(256) append_kernel(const AppendArgs a) {

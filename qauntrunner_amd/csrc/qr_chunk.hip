@@ -16,7 +16,8 @@
 // The 8 PV k-slots of lane quarter q are tokens {4q..4q+3, 16+4q..16+4q+3} of the
 // 32-token tile: the 8 scores that lane already holds for its row after QK.  Each
 // lane owns one row in both results, so the causal mask and the online-softmax
-// rescale are lane-local.  K tiles are staged row-major, V tiles transposed.
+// rescale are lane-local.  K tiles are staged row-major; V tiles are copied from the
+// dims-major V block of the page, which already is the V^T operand layout.
 // Operands are fp16 (bf16 caches are widened to fp16 while staged, exact inside the
 // fp16 range); accumulation and softmax are fp32.
 #include "qr_chunk.hpp"
@@ -77,7 +78,7 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
     constexpr int NK = D / 32;             // QK k-steps
     constexpr int NDT = D / 16;            // PV dim tiles
     constexpr int RS = D * 2 + 16;         // K row stride in LDS (bytes), padded
-    constexpr int TS = kTok * 2 + 8;       // V^T row stride in LDS (bytes), padded
+    constexpr int TS = kTok * 2 + 16;      // V^T row stride in LDS (bytes), padded, 16-byte aligned
     constexpr int TILE_BYTES = kTok * D * 2;          // per plane
     constexpr int CPT = 2 * TILE_BYTES / 16 / 256;    // 16-byte chunks per thread (K then V)
     static_assert(CPT >= 1 && 2 * TILE_BYTES % (16 * 256) == 0, "tile must split evenly over 256 threads");
@@ -131,37 +132,44 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
     }
 
     const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
+    // K rows are token-major; the V block of the page is dims-major ([dim][256 positions]),
+    // so a tile's V^T is D rows of 64 contiguous bytes
     auto load_tile = [&](int t0, U32x4 (&r)[CPT]) {
         const long long phys = p.page_table[t0 >> kPageShift];
-        const char* kb = p.pool + (phys * p.page_elems + head_off + static_cast<long long>(t0 & (kPageTokens - 1)) * D) * 2;
-        const char* vb = kb + p.plane_elems * 2;
+        const int slot0 = t0 & (kPageTokens - 1);
+        const char* kb = p.pool + (phys * p.page_elems + head_off + static_cast<long long>(slot0) * D) * 2;
+        const char* vb = p.pool + (phys * p.page_elems + p.plane_elems + head_off + slot0) * 2;
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
             const int gi = c * 256 + threadIdx.x;          // chunk index over K then V
             const int plane = gi / (TILE_BYTES / 16);
-            const int off = (gi - plane * (TILE_BYTES / 16)) * 16;
-            r[c] = load16((plane ? vb : kb) + off);
+            const int ci = gi - plane * (TILE_BYTES / 16);
+            r[c] = plane ? load16(vb + ((ci >> 2) * kPageTokens + 8 * (ci & 3)) * 2) : load16(kb + ci * 16);
         }
     };
-    auto store_tile = [&](const U32x4 (&r)[CPT], int buf) {
+    auto store_tile = [&](const U32x4 (&r)[CPT], int buf, int t0) {
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
             const int gi = c * 256 + threadIdx.x;
             const int plane = gi / (TILE_BYTES / 16);
-            const int off = (gi - plane * (TILE_BYTES / 16)) * 16;
-            const int tok = off / (D * 2);
-            const int cb = off - tok * D * 2;              // byte offset inside the row
+            const int ci = gi - plane * (TILE_BYTES / 16);
             U32x4 v = r[c];
             if (SRC_BF16) v = U32x4{widen_bf16_pair(v.x), widen_bf16_pair(v.y), widen_bf16_pair(v.z), widen_bf16_pair(v.w)};
             if (plane == 0) {
-                *reinterpret_cast<U32x4*>(lds_k[buf] + tok * RS + cb) = v;
+                const int tok = ci / (D / 8);
+                *reinterpret_cast<U32x4*>(lds_k[buf] + tok * RS + (ci - tok * (D / 8)) * 16) = v;
             } else {
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-                const int d0 = cb / 2;
+                // dim ci/4, positions t0 + 8(ci%4) .. +7; positions past t_end may hold stale
+                // rows and are zeroed so that a zero weight cannot meet a NaN
+                const int first = t0 + 8 * (ci & 3);
+                if (first + 8 > t_end) {
+                    uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    *reinterpret_cast<uint16_t*>(lds_v[buf] + (d0 + i) * TS + tok * 2) =
-                        static_cast<uint16_t>(w4[i >> 1] >> ((i & 1) * 16));
+                    for (int i = 0; i < 8; ++i)
+                        if (first + i >= t_end) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                    v = U32x4{w[0], w[1], w[2], w[3]};
+                }
+                *reinterpret_cast<U32x4*>(lds_v[buf] + (ci >> 2) * TS + 16 * (ci & 3)) = v;
             }
         }
     };
@@ -170,7 +178,7 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
     U32x4 stage[CPT];
     if (ntiles > 0) {
         load_tile(t_begin, stage);
-        store_tile(stage, 0);
+        store_tile(stage, 0, t_begin);
     }
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
@@ -240,7 +248,7 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) acc[j][t] = mma16(a, pb[j], acc[j][t]);
         }
-        if (it + 1 < ntiles) store_tile(stage, buf ^ 1);
+        if (it + 1 < ntiles) store_tile(stage, buf ^ 1, t0 + kTok);
         __syncthreads();
     }
 

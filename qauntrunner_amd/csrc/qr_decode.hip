@@ -72,6 +72,16 @@ __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
 }
 
+typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 mfma_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mfma_bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ mfma_f32x4 mfma16(mfma_f16x8 a, mfma_f16x8 b, mfma_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ mfma_f32x4 mfma16(mfma_bf16x8 a, mfma_bf16x8 b, mfma_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // DT: head_dim fixed at compile time (0: read from the arguments).
 template <typename KT, int GMAX, int DPL, int U, int DT>
 __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p) {
@@ -192,6 +202,10 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
             float v[DPL];
 #pragma unroll
             for (int j = 0; j < NC; ++j) C::widen(vb[u][j], &v[j * EPC]);
+            // rows past the end may hold stale data: a zero weight must not meet a NaN
+            const bool valid = t0 + u * ntg < t_end;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) v[e] = valid ? v[e] : 0.f;
 #pragma unroll
             for (int g = 0; g < GMAX; ++g) {
                 const float pr = fast_exp2(s[u][g] - mref[g]);  // masked rows: exp2(-inf) = 0
@@ -269,6 +283,260 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     }
     __syncthreads();
 
+    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    const size_t row_base = static_cast<size_t>(b) * p.heads;
+    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][g]);
+        float L = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float c = exp2_or_zero(sm_m[w][g] - M, sm_m[w][g]);
+            L += sm_l[w][g] * c;
+            o += sm_acc[w][g][d] * c;
+        }
+        const int h = h0 + g;
+        if (nsplit == 1) {
+            p.out[(row_base + h) * D + d] = o / L;
+        } else {
+            const size_t slot = (row_base + h) * kMaxSplits + split;
+            p.part_acc[slot * D + d] = o;
+            if (d == 0) p.part_ml[slot] = make_float2(M, L);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA decode for 16-bit caches with head_dim 64 or 128 (V stored dims-major).
+//
+// Workgroup = 4 waves, one unit (a kv head and up to 16 of its query heads), one
+// split.  The split is walked in 32-position steps; wave w takes steps w, w+4, ...
+// with its own online softmax, and the four waves are merged through LDS at the end.
+//   QK  S^T[pos][head] = K[pos][dims] . q^T[dims][head]: A = 16 K rows loaded straight
+//       from the page (16 bytes per lane and k-step), B = q held in registers.
+//   PV  O^T[dim][head] += V^T[dim][pos] . P^T[pos][head]: A = 8 consecutive positions
+//       of one dim, a single 16-byte load from the dims-major V block.
+// v_mfma_f32_16x16x32_{f16,bf16} lane layout (checked on gfx950):
+//   A[m = lane%16][k = 8*(lane/16)+i], B[k = 8*(lane/16)+i][n = lane%16],
+//   D[m = 4*(lane/16)+r][n = lane%16].
+// QK M tile mt takes row m as position 8(m/4) + 4mt + m%4, so after QK lane quarter
+// q holds the scores of positions 8q..8q+7 of the step: exactly its PV k-slots.
+// Precision: q and P are split into hi + lo parts of the cache's 16-bit type and
+// every product is two MFMAs with fp32 accumulation, so q and P keep about 22
+// (fp16) or 16 (bf16) significant bits while K and V enter exactly.  q is
+// pre-multiplied per head by the power of two that brings its largest element to at
+// most 2^14 (exact), so fp16 never overflows; the scores are scaled back.
+constexpr int kMfmaGroup = 16;  // query heads per unit on the MFMA path
+#ifndef QR_MFMA_DECODE_BUFFERS
+#define QR_MFMA_DECODE_BUFFERS 2
+#endif
+constexpr int kMfmaBuffers = QR_MFMA_DECODE_BUFFERS;  // register buffers of the step pipeline
+
+#ifndef QR_MFMA_DECODE_WG_PER_CU
+#define QR_MFMA_DECODE_WG_PER_CU 2
+#endif
+constexpr int kMfmaWgPerCu = QR_MFMA_DECODE_WG_PER_CU;  // resident workgroups per CU the registers allow
+
+template <bool BF16, int D>
+__global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(const DecodeK p) {
+    using T = typename std::conditional<BF16, __bf16, _Float16>::type;
+    typedef T vec8 __attribute__((ext_vector_type(8)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int NK = D / 32;   // QK k-steps
+    constexpr int NDT = D / 16;  // PV dim tiles
+    constexpr int kStep = 32;    // positions per step
+
+    const int split = blockIdx.x;
+    const int unit = blockIdx.y;
+    const int b = blockIdx.z;
+    const int seq = p.seq_len[b];
+    const int t_begin = split * p.split_tokens;
+    if (t_begin >= seq) return;
+    const int t_end = min(seq, t_begin + p.split_tokens);
+    const int lane = threadIdx.x & 63;
+    // wave-uniform (SGPR): step positions, and so the page-table entry of a step, are
+    // scalar; a vector load there would make every step wait for all loads in flight
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (kWaves - 1);
+    const int q4 = lane >> 4;
+    const int n = lane & 15;
+
+    int kvh, h0, G;
+    if (p.per_head) {
+        h0 = unit;
+        kvh = static_cast<int>(static_cast<long long>(unit) * p.kv_heads / p.heads);
+        G = 1;
+    } else {
+        const int c = unit % p.head_chunks;
+        kvh = unit / p.head_chunks;
+        h0 = kvh * p.group + c * kMfmaGroup;
+        G = min(kMfmaGroup, p.group - c * kMfmaGroup);
+    }
+    const int* pt = p.page_table + p.pt_off[b];
+    const long long kblk = static_cast<long long>(kvh) * kPageTokens * D;
+    const int krow = 8 * (n >> 2) + (n & 3);  // QK row of this lane in M tile 0 (+4 in tile 1)
+    const int total_steps = (t_end - t_begin + kStep - 1) / kStep;
+    const int nst = total_steps > wave ? (total_steps - wave + kWaves - 1) / kWaves : 0;
+
+    constexpr int NB = kMfmaBuffers;
+    U32x4 kb[NB][2][NK];
+    U32x4 vb[NB][NDT];
+    auto issue = [&](int st, int buf) {
+        const int t0 = t_begin + st * kStep;  // a step never crosses a page
+        const long long phys = pt[t0 >> kPageShift];
+        const int slot0 = t0 & (kPageTokens - 1);
+        const char* kp = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
+        const char* vp = p.pool + (phys * p.page_elems + p.plane_elems + kblk + slot0) * 2;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < NK; ++kk)
+                kb[buf][mt][kk] = load16(kp + ((krow + 4 * mt) * D + 32 * kk + 8 * q4) * 2);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) vb[buf][dt] = load16(vp + ((16 * dt + n) * kPageTokens + 8 * q4) * 2);
+    };
+    if (nst > 0) issue(wave, 0);
+    if (NB == 3 && nst > 0) issue(nst > 1 ? wave + kWaves : wave, 1);
+
+    // ---- q of head h0 + n (zero for padding columns), log2 units, split into hi + lo
+    const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
+    const int hq = min(h0 + n, p.heads - 1);
+    const float qs = n < G ? p.qscale : 0.f;
+    float qf[NK][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // scalar loads: the caller's q needs only 4-byte alignment
+            qf[kk][i] = qb[static_cast<size_t>(hq) * D + 32 * kk + 8 * q4 + i] * qs;
+            amax = fmaxf(amax, fabsf(qf[kk][i]));
+        }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    int qexp = 0;
+    if (!BF16 && amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
+    const float down = ldexpf(1.f, -qexp);
+    const float sscale = ldexpf(1.f, qexp);
+    vec8 qhi[NK], qlo[NK];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = qf[kk][i] * down;
+            const T hi = static_cast<T>(x);
+            qhi[kk][i] = hi;
+            qlo[kk][i] = static_cast<T>(x - static_cast<float>(hi));
+        }
+
+    f32x4 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    auto compute = [&](int st, int buf) {
+        const int t0 = t_begin + st * kStep;
+        f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < NK; ++kk) {
+                const vec8 a = __builtin_bit_cast(vec8, kb[buf][mt][kk]);
+                sc[mt] = mfma16(a, qhi[kk], sc[mt]);
+                sc[mt] = mfma16(a, qlo[kk], sc[mt]);
+            }
+        // scores of positions t0 + 8q4 + i, i = 4mt + r
+        float s[8];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            s[i] = t0 + 8 * q4 + i < t_end ? sc[i >> 2][i & 3] * sscale : -INFINITY;
+            tmax = fmaxf(tmax, s[i]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // lazy rescale: m moves only when the step max exceeds it by more than 2^8,
+        // so P = 2^(s - m) <= 256; the whole wave skips the rescale when no lane needs it
+        const bool grow = tmax > m + 8.f;
+        const bool rescale = grow && m != -INFINITY;
+        if (__builtin_amdgcn_ballot_w64(rescale)) {
+            const float corr = rescale ? fast_exp2(m - tmax) : 1.f;
+            l *= corr;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] *= corr;
+        }
+        if (grow) m = tmax;
+        const float mref = m == -INFINITY ? 0.f : m;
+        vec8 phi, plo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float e = fast_exp2(s[i] - mref);  // masked positions: 2^-inf = 0
+            l += e;
+            const T hi = static_cast<T>(e);
+            phi[i] = hi;
+            plo[i] = static_cast<T>(e - static_cast<float>(hi));
+        }
+        // a partial last step: positions past the end hold stale rows; zero their V
+        // elements so that a zero weight cannot meet a NaN
+        if (t0 + kStep > t_end) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                uint32_t w[4] = {vb[buf][dt].x, vb[buf][dt].y, vb[buf][dt].z, vb[buf][dt].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (t0 + 8 * q4 + i >= t_end) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                vb[buf][dt] = U32x4{w[0], w[1], w[2], w[3]};
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const vec8 a = __builtin_bit_cast(vec8, vb[buf][dt]);
+            acc[dt] = mfma16(a, phi, acc[dt]);
+            acc[dt] = mfma16(a, plo, acc[dt]);
+        }
+    };
+
+    // ---- pipeline over this wave's steps with NB register buffers (NB - 1 steps in
+    // flight ahead of the one computed); every iteration issues the same loads (past
+    // the end it re-reads a step already loaded) so the compiler's load counting stays
+    // exact
+    auto gstep = [&](int i) { return wave + kWaves * min(i, nst - 1); };
+    if (NB == 2) {
+        for (int i = 0; i < nst; i += 2) {
+            issue(gstep(i + 1), 1);
+            compute(gstep(i), 0);
+            if (i + 1 >= nst) break;
+            issue(gstep(i + 2), 0);
+            compute(gstep(i + 1), 1);
+        }
+    } else {
+        for (int i = 0; i < nst; i += 3) {
+            issue(gstep(i + 2), 2);
+            compute(gstep(i), 0);
+            if (i + 1 >= nst) break;
+            issue(gstep(i + 3), 0);
+            compute(gstep(i + 1), 1);
+            if (i + 2 >= nst) break;
+            issue(gstep(i + 4), 1);
+            compute(gstep(i + 2), 2);
+        }
+    }
+
+    // ---- merge the four waves through LDS (l is summed over the lane quarters first)
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    __shared__ float sm_acc[kWaves][kMfmaGroup][D];
+    __shared__ float sm_m[kWaves][kMfmaGroup];
+    __shared__ float sm_l[kWaves][kMfmaGroup];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+        *reinterpret_cast<float4*>(&sm_acc[wave][n][16 * dt + 4 * q4]) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+    if (q4 == 0) {
+        sm_m[wave][n] = m;
+        sm_l[wave][n] = l;
+    }
+    __syncthreads();
     const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
     const size_t row_base = static_cast<size_t>(b) * p.heads;
     for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
@@ -410,12 +678,14 @@ const void* by_dim(int gmax, int head_dim) {
          : by_gmax<KT, U, 0>(gmax);
 }
 
+// 16-bit caches reach this path only with head_dim 16, 32 or 256 (64 and 128 run
+// on MFMA tiles).
 const void* select_kernel(int dtype, int gmax, int head_dim) {
     const bool narrow = head_dim == 16;
     switch (dtype) {
         case QR_DTYPE_F32: return by_dim<float, 2>(gmax, head_dim);
-        case QR_DTYPE_F16: return narrow ? by_gmax<F16Tag, 2, 0>(gmax) : by_dim<F16Tag, 4>(gmax, head_dim);
-        default: return narrow ? by_gmax<BF16Tag, 2, 0>(gmax) : by_dim<BF16Tag, 4>(gmax, head_dim);
+        case QR_DTYPE_F16: return narrow ? by_gmax<F16Tag, 2, 0>(gmax) : by_gmax<F16Tag, 4, 0>(gmax);
+        default: return narrow ? by_gmax<BF16Tag, 2, 0>(gmax) : by_gmax<BF16Tag, 4, 0>(gmax);
     }
 }
 
@@ -453,11 +723,14 @@ int cu_count() {
     return cus;
 }
 
+// The dims-major V layout marks the caches whose decode runs on MFMA tiles.
+bool uses_mfma(const DecodeArgs& a) { return a.geom.v_dims_major != 0; }
+
 int units_of(const DecodeArgs& a, int* gmax) {
     const int kvh = a.geom.kv_heads;
     if (a.heads % kvh == 0) {
         const int group = a.heads / kvh;
-        *gmax = pick_gmax(group);
+        *gmax = uses_mfma(a) ? kMfmaGroup : pick_gmax(group);
         return kvh * ((group + *gmax - 1) / *gmax);
     }
     *gmax = 1;
@@ -480,7 +753,8 @@ DecodePlan plan_decode(const DecodeArgs& a) {
     // about one workgroup per CU, whole pages per split, at most 16 pages per split
     // (measured on MI355X: fewer, longer splits beat more resident workgroups)
     (void)blocks_per_cu;
-    long long pps = std::max<long long>(1, work / cu_count());
+    const int slots = cu_count() * (uses_mfma(a) ? kMfmaWgPerCu : 1);
+    long long pps = std::max<long long>(1, work / slots);
     pps = std::min<long long>(pps, 16);
     pps = std::max<long long>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
     pps = std::min<long long>(pps, max_pages);
@@ -526,7 +800,15 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
         k.pt_off[i] = a.pt_off[i];
     }
     if (pl.max_splits > kMaxSplits) return hipErrorInvalidValue;
-    const void* fn = select_kernel(a.dtype, gmax, a.geom.head_dim);
+    const void* fn;
+    if (uses_mfma(a)) {
+        const bool bf = a.dtype == QR_DTYPE_BF16;
+        fn = a.geom.head_dim == 128
+            ? (bf ? reinterpret_cast<const void*>(&decode_mfma_kernel<true, 128>) : reinterpret_cast<const void*>(&decode_mfma_kernel<false, 128>))
+            : (bf ? reinterpret_cast<const void*>(&decode_mfma_kernel<true, 64>) : reinterpret_cast<const void*>(&decode_mfma_kernel<false, 64>));
+    } else {
+        fn = select_kernel(a.dtype, gmax, a.geom.head_dim);
+    }
     void* args[] = {&k};
     hipError_t e = hipLaunchKernel(fn, dim3(pl.max_splits, k.units, a.nb), dim3(kThreads), args, 0, stream);
     if (e != hipSuccess) return e;

@@ -10,15 +10,28 @@ namespace qr {
 //   page = planes x kv_heads x kPageTokens x head_dim
 // plane 0 holds K, plane 1 holds V (GQA cache); the MLA cache has one plane with
 // kv_heads = 1 and head_dim = latent width.  Inside a plane each kv head owns a
-// contiguous [kPageTokens][head_dim] block, so one (page, kv head) is a single
-// contiguous stream of 256 rows.
+// contiguous block of kPageTokens x head_dim elements: [token][dim] (one
+// contiguous stream of 256 rows), or, for the V plane when v_dims_major is set,
+// [dim][token], so that the 16-bit MFMA kernels read V^T operands (8 consecutive
+// tokens of one dim) as single 16-byte loads.
 struct PageGeom {
     int planes;
     int kv_heads;
     int head_dim;
+    int v_dims_major = 0;
     __host__ __device__ long long plane_elems() const { return (long long)kv_heads * kPageTokens * head_dim; }
     __host__ __device__ long long page_elems() const { return plane_elems() * planes; }
+    // element offset of (plane, kv head, slot, dim) inside page `phys`
+    __host__ __device__ long long offset(long long phys, int plane, int kvh, int slot, int d) const {
+        const long long blk = phys * page_elems() + plane * plane_elems() + (long long)kvh * kPageTokens * head_dim;
+        return plane == 1 && v_dims_major ? blk + (long long)d * kPageTokens + slot : blk + (long long)slot * head_dim + d;
+    }
 };
+// 16-bit GQA caches with head_dim 64 or 128 keep V dims-major (their decode and
+// chunk kernels run on MFMA tiles).
+inline bool kv_v_dims_major(int dtype, int head_dim) {
+    return dtype != QR_DTYPE_F32 && (head_dim == 64 || head_dim == 128);
+}
 
 // Writes rows pos0..pos0+n-1 of `planes` source arrays into their pages.
 // src[p] is [n][src_stride] of src_dtype; only the first row_len[p] elements of

@@ -101,6 +101,59 @@ def test_decode_shapes(gpu, heads, kv_heads, D, seq):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,D,seq", [
+    (64, 8, 128, 1300),  # G = 8 (70B shape)
+    (32, 2, 128, 600),   # G = 16: one full MFMA column block
+    (48, 2, 128, 900),   # G = 24: two head chunks (16 + 8)
+    (12, 4, 64, 2049),   # G = 3, head_dim 64
+    (14, 2, 128, 257),   # G = 7, one position into the second page
+    (6, 4, 64, 300),     # uneven GQA map, one query head per workgroup
+    (1, 1, 64, 1),       # single position
+])
+def test_decode_16bit_mfma_shapes(gpu, dtype, heads, kv_heads, D, seq):
+    """16-bit caches with head_dim 64/128 decode on MFMA tiles (V stored dims-major)
+    with hi/lo-split q and P: still the fp32-accumulation tolerance."""
+    q = normal(seq + 7, heads * D)
+    Kb, K = to_dtype_bits(normal(seq + 8, (seq, kv_heads * D)), dtype)
+    Vb, V = to_dtype_bits(normal(seq + 9, (seq, kv_heads * D)), dtype)
+    scale = 1 / math.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, seq + 5, kv_dtype=dtype) as kv:
+        kv.AppendRange(0, 0, Kb, Vb, src_dtype=dtype)
+        kr, vr = kv.Read(0, 0, seq)
+        assert np.array_equal(kr, Kb) and np.array_equal(vr, Vb)  # layout round trip
+        check_decode(kv.Attention(0, seq - 1, q, scale), K, V, q, heads, kv_heads, D, scale,
+                     f"{dtype} H{heads}/Hkv{kv_heads}/D{D}/seq{seq}")
+        if seq > 3:
+            p = seq // 3
+            check_decode(kv.Attention(0, p, q, scale), K[:p + 1], V[:p + 1], q, heads, kv_heads, D, scale,
+                         f"{dtype} H{heads}/Hkv{kv_heads}/D{D}/pos{p}")
+
+
+@pytest.mark.parametrize("dtype,D", [("f32", 128), ("f16", 128), ("bf16", 64), ("f16", 32)])
+def test_stale_nan_rows_past_the_position_are_ignored(gpu, dtype, D):
+    """Rows past the attended position that still hold NaN (an earlier sequence,
+    then Truncate) never reach the result: the reference reads rows 0..pos only."""
+    heads, kv_heads, n, pos = 8, 2, 600, 300
+    K, V = normal(120, (n, kv_heads * D)), normal(121, (n, kv_heads * D))
+    Kb, Kd = to_dtype_bits(K, dtype)
+    Vb, Vd = to_dtype_bits(V, dtype)
+    nanb = np.full_like(Kb, np.nan) if dtype == "f32" else np.full_like(Kb, 0x7E00 if dtype == "f16" else 0x7FC0)
+    q = normal(122, heads * D)
+    scale = 1 / math.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, n, kv_dtype=dtype) as kv:
+        kv.AppendRange(0, 0, nanb, nanb, src_dtype=dtype)
+        kv.Truncate(0)
+        kv.AppendRange(0, 0, Kb[:pos + 1], Vb[:pos + 1], src_dtype=dtype)
+        got = kv.Attention(0, pos, q, scale)
+        assert np.isfinite(got).all()
+        check_decode(got, Kd[:pos + 1], Vd[:pos + 1], q, heads, kv_heads, D, scale, f"stale NaN {dtype} D{D}")
+        if D in (64, 128) and dtype != "f32":  # chunk path: queries pos-3..pos over the same pages
+            qs = normal(123, (4, heads * D))
+            out = kv.AttentionChunk(0, pos - 3, qs, scale)
+            assert np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_16bit_append_bits_and_decode(gpu, dtype):
     """fp32 rows appended into a 16-bit cache take the reference codec's bits
     (FloatToF16 / FloatToBf16); attention then runs on the exactly decoded values."""
