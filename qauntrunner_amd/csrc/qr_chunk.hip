@@ -7,41 +7,32 @@
 //
 // A row is one (query, query head) pair; the G = heads/kv_heads heads of one kv
 // head and a block of consecutive queries form the rows of a workgroup, so every
-// K/V tile staged in LDS serves them all.  Workgroup = 4 waves x NT x 16 rows.
-// v_mfma_f32_16x16x32_f16 (lane layout verified on gfx950):
-//   A[m = lane%16][k = 8*(lane/16)+i], B[k = 8*(lane/16)+i][n = lane%16],
-//   D[m = 4*(lane/16)+r][n = lane%16].
-//   QK: S^T[token][row] = K[token][dims] . Q^T[dims][row]      (M tokens, N rows)
-//   PV: O^T[dim][row]  += V^T[dim][tokens] . P^T[tokens][row]   (M dims,   N rows)
-// The 8 PV k-slots of lane quarter q are tokens {4q..4q+3, 16+4q..16+4q+3} of the
-// 32-token tile: the 8 scores that lane already holds for its row after QK.  Each
-// lane owns one row in both results, so the causal mask and the online-softmax
-// rescale are lane-local.  K tiles are staged row-major; V tiles are copied from the
-// dims-major V block of the page, which already is the V^T operand layout.
-// Operands are fp16 (bf16 caches are widened to fp16 while staged, exact inside the
-// fp16 range); accumulation and softmax are fp32.
+// K/V tile staged in LDS serves them all.  Workgroup = 4 waves x NT x 16 rows; each
+// wave owns its rows for the whole split, so waves never exchange data inside a tile.
+//   QK: S^T[pos][row] = K[pos][dims] . Q^T[dims][row]     (M positions, N rows)
+//   PV: O^T[dim][row] += V^T[dim][pos] . P^T[pos][row]     (M dims,      N rows)
+// Tiles of 64 positions are copied into LDS by buffer-load DMA (K row-major, V^T
+// straight from the dims-major V block of the page), NSTAGE-buffered, with XOR
+// swizzles that keep the 16 rows of every MFMA operand read on distinct banks.  QK
+// row m of M tile mt is position 32(mt/2) + 8(m/4) + 4(mt%2) + m%4, so after QK lane
+// quarter q holds the scores of positions 32ks + 8q .. +7, its PV k-slots of step ks.
+// Operands stay in the cache's 16-bit type (no conversion); q enters as hi + lo parts
+// when its own type is not the cache's (fp32 queries keep ~22 or ~16 bits), P is
+// rounded to the cache type; accumulation and softmax are fp32.  Row sums come from
+// the MFMA too (a ones operand), consistent with the rounded P of the numerator.
+// The causal mask is applied only on tiles that reach past the block's first query.
 #include "qr_chunk.hpp"
+#include "qr_mfma.hpp"
 
 #include <algorithm>
 
 namespace qr {
 namespace {
 
-constexpr int kTok = 32;  // tokens per tile
-
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f32x4_t mma16(f16x8_t a, f16x8_t b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t widen_bf16_pair(uint32_t w) {
-    const _Float16 lo = static_cast<_Float16>(__uint_as_float(w << 16));
-    const _Float16 hi = static_cast<_Float16>(__uint_as_float(w & 0xFFFF0000u));
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
-}
+constexpr int kTile = 64;  // positions per tile
+#ifndef QR_CHUNK_MAX_NT
+#define QR_CHUNK_MAX_NT 2
+#endif
 
 __device__ __forceinline__ float load_q(const void* q, int dtype, size_t i) {
     switch (dtype) {
@@ -69,32 +60,37 @@ struct ChunkK {
     float2* part_ml;         // [nq*heads][splits]
     float qscale;            // scale * log2(e)
     int queries_per_block;
-    int split_tokens;
+    int split_tokens;        // multiple of kTile
     int splits;
 };
 
-template <bool SRC_BF16, int D, int NT>
-__global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
-    constexpr int NK = D / 32;             // QK k-steps
-    constexpr int NDT = D / 16;            // PV dim tiles
-    constexpr int RS = D * 2 + 16;         // K row stride in LDS (bytes), padded
-    constexpr int TS = kTok * 2 + 16;      // V^T row stride in LDS (bytes), padded, 16-byte aligned
-    constexpr int TILE_BYTES = kTok * D * 2;          // per plane
-    constexpr int CPT = 2 * TILE_BYTES / 16 / 256;    // 16-byte chunks per thread (K then V)
-    static_assert(CPT >= 1 && 2 * TILE_BYTES % (16 * 256) == 0, "tile must split evenly over 256 threads");
+// BF16: cache element type; NT: 16-row N tiles per wave; NSTAGE: LDS tile buffers;
+// QSPLIT: q is not exact in the cache type and enters as hi + lo parts.
+template <bool BF16, int D, int NT, int NSTAGE, bool QSPLIT>
+__global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const ChunkK p) {
+    using T = typename std::conditional<BF16, __bf16, _Float16>::type;
+    typedef T vec8 __attribute__((ext_vector_type(8)));
+    constexpr int NK = D / 32;               // QK k-steps
+    constexpr int NDT = D / 16;              // PV dim tiles
+    constexpr int RB = D * 2;                // K row bytes
+    constexpr int KB = kTile * RB;           // K tile bytes
+    constexpr int VB = D * kTile * 2;        // V^T tile bytes (D rows of 128 bytes)
+    constexpr int KI = KB / 1024 / 4;        // K DMA instructions per wave and tile
+    constexpr int VI = VB / 1024 / 4;        // V DMA instructions per wave and tile
+    constexpr int PER_TILE = KI + VI;        // vector-memory ops per wave and tile
+    static_assert(KI >= 1 && VI >= 1, "tile must split over 4 waves");
 
-    __shared__ __attribute__((aligned(16))) char lds_k[2][kTok * RS];
-    __shared__ __attribute__((aligned(16))) char lds_v[2][D * TS];
+    __shared__ __attribute__((aligned(1024))) char lds[NSTAGE][KB + VB];
 
     const int split = blockIdx.x;
     const int qblk = blockIdx.y;
     const int kvh = blockIdx.z;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
     const int q4 = lane >> 4;
     const int col = lane & 15;
 
-    // rows of this lane, one per N tile
+    // rows of this lane, one per N tile: (query, head) = (rho >> log2 G, rho & (G - 1))
     const int q_first = qblk * p.queries_per_block;
     int row_q[NT], row_h[NT];
     bool row_on[NT];
@@ -108,159 +104,221 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
     const int q_last = min(p.nq, q_first + p.queries_per_block) - 1;
     const int t_begin = split * p.split_tokens;
     const int t_end = min(t_begin + p.split_tokens, p.pos0 + q_last + 1);  // causal bound of the block
+    const int ntiles = t_end > t_begin ? (t_end - t_begin + kTile - 1) / kTile : 0;
+    const int unmasked_end = p.pos0 + q_first + 1;  // positions below it are seen by every row
 
-    // Q^T operands (fp16), rows beyond the chunk read row 0 and are never written
-    f16x8_t qv[NT][NK];
+    // ---- DMA of tile `it` into stage it % NSTAGE.  K: row t of the tile at t*RB, its
+    // chunk c at slot c ^ fk(t); V^T: dim row d at KB + 128 d, chunk c (positions
+    // 8c..8c+7) at slot c ^ ((d >> 1) & 7).  Rows past the end read zeros (K: buffer
+    // range; V: chunks wholly past the end are sent out of range, the one partial
+    // chunk per row is cleared after it lands).
+    const long long kblk = static_cast<long long>(kvh) * kPageTokens * D;
+    const int vdim = lane >> 3;                          // dim row inside a V instruction
+    const int vslot = lane & 7;
+    const int vchunk = vslot ^ ((vdim >> 1) & 3) ^ ((wave & 1) << 2);  // n & 1 == wave & 1
+    auto dma = [&](int it) {
+        const int t0 = t_begin + it * kTile;
+        const long long phys = p.page_table[t0 >> kPageShift];
+        const int slot0 = t0 & (kPageTokens - 1);
+        const int nvalid = min(kTile, t_end - t0);
+        char* dst = lds[it % NSTAGE];
+        const char* kbase = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
+        const char* vbase = p.pool + (phys * p.page_elems + p.plane_elems + kblk + slot0) * 2;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, nvalid * RB, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbase), 0, (D - 1) * kPageTokens * 2 + kTile * 2, kBufferFlags);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int n = wave + 4 * i;
+            int r, c;
+            if (D == 128) {  // 4 rows per instruction, 16 chunks per row; fk(t) = t0 t1 t3 t4
+                r = 4 * n + (lane >> 4);
+                c = (lane & 15) ^ ((r & 3) | ((r >> 1) & 12));
+            } else {         // 8 rows per instruction, 8 chunks per row; fk(t) = t1 t3 t4
+                r = 8 * n + (lane >> 3);
+                c = (lane & 7) ^ (((r >> 1) & 1) | ((r >> 2) & 6));
+            }
+            buffer_load_lds16(rk, dst + 1024 * n, r * RB + 16 * c, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int n = wave + 4 * i;                      // dims 8n .. 8n+7
+            const uint32_t off = (vdim * kPageTokens * 2 + 16 * vchunk) + (8 * vchunk >= nvalid ? 0x40000000u : 0u);
+            buffer_load_lds16(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
+        }
+    };
+
+    // ---- q rows as B operands (dims 32kk + 8q4 .. +8), scaled per row by a power of two
+    // so that fp16 cannot overflow; log2-unit score scale per row
+    vec8 qhi[NT][NK], qlo[NT][NK];
+    float sscale[NT];
+    if (ntiles > 0) dma(0);
+    if (NSTAGE > 2 && ntiles > 1) dma(1);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const size_t qrow = (static_cast<size_t>(row_on[j] ? row_q[j] : 0) * p.heads + row_h[j]) * D;
+        float x[NK][8];
+        float amax = 0.f;
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                qv[j][kk][i] = static_cast<_Float16>(load_q(p.q, p.q_dtype, qrow + 32 * kk + 8 * q4 + i));
+            for (int i = 0; i < 8; ++i) {
+                x[kk][i] = load_q(p.q, p.q_dtype, qrow + 32 * kk + 8 * q4 + i);
+                amax = fmaxf(amax, fabsf(x[kk][i]));
+            }
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        int qexp = 0;
+        if (!BF16 && amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
+        const float down = ldexpf(1.f, -qexp);
+        sscale[j] = p.qscale * ldexpf(1.f, qexp);
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = x[kk][i] * down;
+                const T hi = static_cast<T>(v);
+                qhi[j][kk][i] = hi;
+                if (QSPLIT) qlo[j][kk][i] = static_cast<T>(v - static_cast<float>(hi));
+            }
     }
+    vec8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = static_cast<T>(1.f);
 
-    f32x4_t acc[NT][NDT];
-    float m[NT], l[NT];
+    f32x4_t acc[NT][NDT], accl[NT];
+    float m[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         m[j] = -INFINITY;
-        l[j] = 0.f;
+        accl[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < NDT; ++t) acc[j][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    // QK row m of M tile mt is position 32(mt/2) + 8(m/4) + 4(mt%2) + m%4, so lane quarter
+    // q4 ends with positions 32ks + 8q4 .. +7: its PV k-slots of step ks in order.
+    const int kq_off = (32 * 0 + 8 * (col >> 2) + (col & 3)) * RB;  // + (32(mt/2) + 4(mt%2)) * RB
+    const int kq_swz = D == 128 ? col : ((col >> 1) & 7);           // fk of every row this lane reads
+    const int pv_swz = (col >> 1) & 7;                              // V^T slot swizzle of dim row 16dt + col
 
-    const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
-    // K rows are token-major; the V block of the page is dims-major ([dim][256 positions]),
-    // so a tile's V^T is D rows of 64 contiguous bytes
-    auto load_tile = [&](int t0, U32x4 (&r)[CPT]) {
-        const long long phys = p.page_table[t0 >> kPageShift];
-        const int slot0 = t0 & (kPageTokens - 1);
-        const char* kb = p.pool + (phys * p.page_elems + head_off + static_cast<long long>(slot0) * D) * 2;
-        const char* vb = p.pool + (phys * p.page_elems + p.plane_elems + head_off + slot0) * 2;
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int gi = c * 256 + threadIdx.x;          // chunk index over K then V
-            const int plane = gi / (TILE_BYTES / 16);
-            const int ci = gi - plane * (TILE_BYTES / 16);
-            r[c] = plane ? load16(vb + ((ci >> 2) * kPageTokens + 8 * (ci & 3)) * 2) : load16(kb + ci * 16);
-        }
-    };
-    auto store_tile = [&](const U32x4 (&r)[CPT], int buf, int t0) {
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int gi = c * 256 + threadIdx.x;
-            const int plane = gi / (TILE_BYTES / 16);
-            const int ci = gi - plane * (TILE_BYTES / 16);
-            U32x4 v = r[c];
-            if (SRC_BF16) v = U32x4{widen_bf16_pair(v.x), widen_bf16_pair(v.y), widen_bf16_pair(v.z), widen_bf16_pair(v.w)};
-            if (plane == 0) {
-                const int tok = ci / (D / 8);
-                *reinterpret_cast<U32x4*>(lds_k[buf] + tok * RS + (ci - tok * (D / 8)) * 16) = v;
-            } else {
-                // dim ci/4, positions t0 + 8(ci%4) .. +7; positions past t_end may hold stale
-                // rows and are zeroed so that a zero weight cannot meet a NaN
-                const int first = t0 + 8 * (ci & 3);
-                if (first + 8 > t_end) {
-                    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        if (first + i >= t_end) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                    v = U32x4{w[0], w[1], w[2], w[3]};
-                }
-                *reinterpret_cast<U32x4*>(lds_v[buf] + (ci >> 2) * TS + 16 * (ci & 3)) = v;
-            }
-        }
-    };
-
-    const int ntiles = t_end > t_begin ? (t_end - t_begin + kTok - 1) / kTok : 0;
-    U32x4 stage[CPT];
-    if (ntiles > 0) {
-        load_tile(t_begin, stage);
-        store_tile(stage, 0, t_begin);
-    }
-    __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
-        const int t0 = t_begin + it * kTok;
-        if (it + 1 < ntiles) load_tile(t0 + kTok, stage);  // in flight during the MFMAs
+        const int t0 = t_begin + it * kTile;
+        // tile `it` landed (the tiles after it stay in flight); the stage refilled next
+        // was consumed in the previous iteration
+        if (NSTAGE > 2 && it + 1 < ntiles) wait_vmcnt<PER_TILE>();
+        else wait_dma();
+        lds_barrier();
+        if (it + NSTAGE - 1 < ntiles) dma(it + NSTAGE - 1);
+        const char* kt = lds[it % NSTAGE];
+        const char* vt = kt + KB;
+        const int nvalid = min(kTile, t_end - t0);
+        if (nvalid & 7) {
+            // the partial V chunk of every dim row: clear positions past the end
+            const int cp = nvalid >> 3;
+            for (int d = threadIdx.x; d < D; d += 256) {
+                uint32_t* w = reinterpret_cast<uint32_t*>(const_cast<char*>(vt) + d * 128 + 16 * (cp ^ ((d >> 1) & 7)));
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (8 * cp + i >= nvalid) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+            }
+            lds_barrier();
+        }
 
-        // QK
-        f32x4_t sc[NT][2];
+        // ---- QK
+        f32x4_t sc[NT][4];
 #pragma unroll
-        for (int j = 0; j < NT; ++j) sc[j][0] = sc[j][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const char* row = lds_k[buf] + (16 * mt + col) * RS + 16 * q4;
+            for (int mt = 0; mt < 4; ++mt) sc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const char* row = kt + kq_off + (32 * (mt >> 1) + 4 * (mt & 1)) * RB;
 #pragma unroll
             for (int kk = 0; kk < NK; ++kk) {
-                const f16x8_t a = *reinterpret_cast<const f16x8_t*>(row + 64 * kk);
+                const vec8 a = *reinterpret_cast<const vec8*>(row + 16 * ((4 * kk + q4) ^ kq_swz));
 #pragma unroll
-                for (int j = 0; j < NT; ++j) sc[j][mt] = mma16(a, qv[j][kk], sc[j][mt]);
+                for (int j = 0; j < NT; ++j) {
+                    sc[j][mt] = mfma16(a, qhi[j][kk], sc[j][mt]);
+                    if (QSPLIT) sc[j][mt] = mfma16(a, qlo[j][kk], sc[j][mt]);
+                }
             }
         }
-        // causal mask + online softmax, one row per lane and N tile
-        f16x8_t pb[NT];
+
+        // ---- causal mask and sequence end, only on tiles that reach past the block's
+        // first query or the end (wave-uniform, one or two tiles per workgroup)
+        if (t0 + kTile > unmasked_end || t0 + kTile > t_end) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const int lim = min(t_end - 1, p.pos0 + row_q[j]);  // last position row j sees
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int tok = t0 + 32 * (mt >> 1) + 8 * q4 + 4 * (mt & 1) + r;
+                        sc[j][mt][r] = tok <= lim ? sc[j][mt][r] : -INFINITY;
+                    }
+            }
+        }
+
+        // ---- online softmax per row: lazy rescale (m moves when the tile max exceeds it
+        // by more than 2^8, so P <= 256), one wave-uniform check for all rows of the lane
+        float ts[NT];
+        bool grow[NT];
+        bool any_rescale = false;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            const int qpos = p.pos0 + row_q[j];
-            float s[8];
             float tmax = -INFINITY;
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int tok = t0 + 16 * mt + 4 * q4 + r;
-                    const float v = (tok < t_end && tok <= qpos) ? sc[j][mt][r] * p.qscale : -INFINITY;
-                    s[4 * mt + r] = v;
-                    tmax = fmaxf(tmax, v);
-                }
+            for (int mt = 0; mt < 4; ++mt)
+                tmax = fmaxf(tmax, fmaxf(fmaxf(sc[j][mt][0], sc[j][mt][1]), fmaxf(sc[j][mt][2], sc[j][mt][3])));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            if (tmax > m[j]) {
-                const float corr = m[j] == -INFINITY ? 0.f : fast_exp2(m[j] - tmax);
-                l[j] *= corr;
+            ts[j] = tmax * sscale[j];
+            grow[j] = ts[j] > m[j] + 8.f;
+            any_rescale |= grow[j] && m[j] != -INFINITY;
+        }
+        if (__builtin_amdgcn_ballot_w64(any_rescale)) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const float corr = grow[j] && m[j] != -INFINITY ? fast_exp2(m[j] - ts[j]) : 1.f;
+                accl[j] *= corr;
 #pragma unroll
                 for (int t = 0; t < NDT; ++t) acc[j][t] *= corr;
-                m[j] = tmax;
-            }
-            const float mref = m[j] == -INFINITY ? 0.f : m[j];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float e = fast_exp2(s[i] - mref);
-                l[j] += e;
-                pb[j][i] = static_cast<_Float16>(e);
             }
         }
-        // PV
-        const char* vcol = lds_v[buf] + col * TS + 8 * q4;
+        vec8 pb[NT][2];
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-            const char* rp = vcol + 16 * t * TS;
-            const uint2 lo = *reinterpret_cast<const uint2*>(rp);
-            const uint2 hi = *reinterpret_cast<const uint2*>(rp + 32);
-            const uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
-            f16x8_t a;
+        for (int j = 0; j < NT; ++j) {
+            if (grow[j]) m[j] = ts[j];
+            const float mneg = m[j] == -INFINITY ? 0.f : -m[j];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                a[i] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w4[i >> 1] >> ((i & 1) * 16)));
+            for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int j = 0; j < NT; ++j) acc[j][t] = mma16(a, pb[j], acc[j][t]);
+                for (int r = 0; r < 4; ++r)
+                    pb[j][mt >> 1][4 * (mt & 1) + r] = static_cast<T>(fast_exp2(fmaf(sc[j][mt][r], sscale[j], mneg)));
         }
-        if (it + 1 < ntiles) store_tile(stage, buf ^ 1, t0 + kTok);
-        __syncthreads();
+
+        // ---- PV (and the row sums: a ones operand turns the MFMA into sum over positions)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) accl[j] = mfma16(ones, pb[j][ks], accl[j]);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const vec8 a = *reinterpret_cast<const vec8*>(vt + (16 * dt + col) * 128 + 16 * ((4 * ks + q4) ^ pv_swz));
+#pragma unroll
+                for (int j = 0; j < NT; ++j) acc[j][dt] = mfma16(a, pb[j][ks], acc[j][dt]);
+            }
+        }
     }
 
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        l[j] += __shfl_xor(l[j], 16);
-        l[j] += __shfl_xor(l[j], 32);
         if (!row_on[j]) continue;
+        const float l = accl[j][0];
         const size_t r = static_cast<size_t>(row_q[j]) * p.heads + row_h[j];
         if (p.splits == 1) {
             float* o = p.out + r * D;
-            const float inv = 1.f / l[j];
+            const float inv = 1.f / l;
 #pragma unroll
             for (int t = 0; t < NDT; ++t)
                 *reinterpret_cast<float4*>(o + 16 * t + 4 * q4) =
@@ -272,7 +330,7 @@ __global__ void __launch_bounds__(256) chunk_mfma_kernel(const ChunkK p) {
             for (int t = 0; t < NDT; ++t)
                 *reinterpret_cast<float4*>(o + 16 * t + 4 * q4) =
                     make_float4(acc[j][t][0], acc[j][t][1], acc[j][t][2], acc[j][t][3]);
-            if (q4 == 0) p.part_ml[slot] = make_float2(m[j], l[j]);
+            if (q4 == 0) p.part_ml[slot] = make_float2(m[j], l);
         }
     }
 }
@@ -315,14 +373,29 @@ int cu_total() {
     return n;
 }
 
-template <bool BF, int D>
-hipError_t launch_nt(const ChunkK& k, int nt, dim3 grid, hipStream_t s) {
-    switch (nt) {
-        case 1: hipLaunchKernelGGL((chunk_mfma_kernel<BF, D, 1>), grid, dim3(256), 0, s, k); break;
-        case 2: hipLaunchKernelGGL((chunk_mfma_kernel<BF, D, 2>), grid, dim3(256), 0, s, k); break;
-        default: hipLaunchKernelGGL((chunk_mfma_kernel<BF, D, 4>), grid, dim3(256), 0, s, k); break;
+template <bool BF, int D, int NT, int NSTAGE>
+hipError_t launch_q(const ChunkK& k, bool qsplit, dim3 grid, hipStream_t s) {
+    if constexpr (NT == 4 && D == 128) {  // hi + lo queries there would spill: the plan never asks
+        if (qsplit) return hipErrorInvalidValue;
+    } else {
+        if (qsplit) {
+            hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, true>), grid, dim3(256), 0, s, k);
+            return hipGetLastError();
+        }
     }
+    hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, false>), grid, dim3(256), 0, s, k);
     return hipGetLastError();
+}
+
+// NT 4 and 2 (prefill-sized query blocks) are MFMA-bound and double buffer; NT 1 (a
+// few queries, e.g. speculative verify) streams the cache and keeps three tiles in LDS.
+template <bool BF, int D>
+hipError_t launch_nt(const ChunkK& k, int nt, bool qsplit, dim3 grid, hipStream_t s) {
+    switch (nt) {
+        case 1: return launch_q<BF, D, 1, 3>(k, qsplit, grid, s);
+        case 2: return launch_q<BF, D, 2, 2>(k, qsplit, grid, s);
+        default: return launch_q<BF, D, 4, 2>(k, qsplit, grid, s);
+    }
 }
 
 }  // namespace
@@ -338,7 +411,8 @@ ChunkPlan plan_chunk(const ChunkArgs& a) {
     const int g = a.heads / a.geom.kv_heads;
     const int total = a.pos0 + a.nq;  // tokens attended by the last query
     // rows per workgroup: up to 256 (4 queries' worth of heads per wave and N tile)
-    int nt = 4;
+    // (hi + lo queries at head_dim 128 need the registers of two N tiles)
+    int nt = QR_CHUNK_MAX_NT;
     while (nt > 1 && (64 * nt) / g > std::max(1, a.nq)) nt >>= 1;
     pl.nt = nt;
     pl.queries_per_block = std::max(1, 64 * nt / g);
@@ -346,8 +420,8 @@ ChunkPlan plan_chunk(const ChunkArgs& a) {
     const int units = qblocks * a.geom.kv_heads;
     // split the keys when there are too few (query block, kv head) units to fill the GPU
     int splits = 1;
-    if (units < cu_total()) splits = std::min((cu_total() + units - 1) / units, (total + kTok - 1) / kTok);
-    int split_tokens = ((total + splits - 1) / splits + kTok - 1) / kTok * kTok;
+    if (units < cu_total()) splits = std::min((cu_total() + units - 1) / units, (total + kTile - 1) / kTile);
+    int split_tokens = ((total + splits - 1) / splits + kTile - 1) / kTile * kTile;
     splits = (total + split_tokens - 1) / split_tokens;
     pl.splits = splits;
     pl.split_tokens = split_tokens;
@@ -385,9 +459,12 @@ hipError_t launch_chunk(const ChunkArgs& a, const ChunkPlan& pl, void* workspace
     k.splits = pl.splits;
     const dim3 grid(pl.splits, pl.qblocks, a.geom.kv_heads);
     const bool bf = a.kv_dtype == QR_DTYPE_BF16;
+    const bool qsplit = a.q_dtype != a.kv_dtype;  // q not exact in the cache's 16-bit type
     hipError_t e;
-    if (a.geom.head_dim == 128) e = bf ? launch_nt<true, 128>(k, pl.nt, grid, stream) : launch_nt<false, 128>(k, pl.nt, grid, stream);
-    else e = bf ? launch_nt<true, 64>(k, pl.nt, grid, stream) : launch_nt<false, 64>(k, pl.nt, grid, stream);
+    if (a.geom.head_dim == 128)
+        e = bf ? launch_nt<true, 128>(k, pl.nt, qsplit, grid, stream) : launch_nt<false, 128>(k, pl.nt, qsplit, grid, stream);
+    else
+        e = bf ? launch_nt<true, 64>(k, pl.nt, qsplit, grid, stream) : launch_nt<false, 64>(k, pl.nt, qsplit, grid, stream);
     if (e != hipSuccess) return e;
     if (after_split && (e = hipEventRecord(after_split, stream)) != hipSuccess) return e;
     if (pl.splits == 1) return hipSuccess;

@@ -11,6 +11,7 @@
 //   unnormalised u) is merged across splits by mla_combine_kernel.  This path
 //   serves every other shape and the fp32 cache.
 #include "qr_mla.hpp"
+#include "qr_mfma.hpp"
 
 #include <algorithm>
 #include <type_traits>
@@ -178,12 +179,8 @@ constexpr int kMHeads = 32;                // heads per workgroup
 constexpr int kMfmaLora = 512;
 constexpr int kScoreStride = kMTile + 4;   // floats per head row of the score buffer
 constexpr float kRescaleSlack = 8.f;       // log2 units
-constexpr int kBufferFlags = 0x00020000;   // raw buffer resource word 3 (gfx9 family)
 
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_ptr;
 
 __device__ __forceinline__ int row_swizzle(int r) {
@@ -221,34 +218,6 @@ template <> struct PvType<true> {
     typedef __bf16 vec __attribute__((ext_vector_type(8)));
     __device__ static f32x4_t mma(vec a, vec b, f32x4_t c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 };
-
-// Workgroup barrier ordering LDS only.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-// Workgroup barrier for data written with ds_write while an LDS-DMA is in flight:
-// it waits for this wave's LDS instructions (lgkmcnt) only.  A release fence
-// would also wait for the DMA (its LDS writes count as vector-memory loads).
-__device__ __forceinline__ void lds_barrier_dma_in_flight() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// s_waitcnt vmcnt(0): this wave's LDS-DMA writes have landed.
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
-// ... lds).  Written as inline asm so that the compiler, which cannot tell the LDS
-// range a DMA writes, does not insert waits for it before unrelated LDS reads;
-// completion is awaited explicitly with wait_dma() before the data is read.
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, const char* lds, uint32_t voffset,
-                                                  uint32_t soffset) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)lds)));
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
-}
 
 struct MlaMK {
     const char* pool;

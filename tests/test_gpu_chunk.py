@@ -3,9 +3,10 @@
 Reference semantics: query i at position pos0+i equals a PagedKvCache.Attention
 call at that position over rows 0..pos0+i (StreamingEngine.cs:831-836,
 SpeculativeRunner.cs:85-93); the oracle is run on the exactly decoded 16-bit values.
-16-bit caches run on MFMA tiles with fp16 operands (bf16 values widened exactly,
-P rounded to fp16): tolerance max-abs <= 1e-3 and rel-L2 <= 5e-3 for bf16 caches,
-<= 1e-3 for fp16 caches.  Both sides' errors against fp64 are printed.
+16-bit caches run on MFMA tiles in the cache's own type (queries of another type as
+hi + lo parts, P rounded to the cache type): tolerance max-abs <= 1e-3 and rel-L2
+<= 5e-3 for bf16 caches, <= 1e-3 for fp16 caches.  Both sides' errors against fp64
+are printed.
 """
 import math
 
@@ -73,16 +74,17 @@ def test_c4_speculative_verify_fp16(gpu):
 @pytest.mark.parametrize("dtype,heads,kv_heads,D,pos0,nq,q_dtype", [
     ("f16", 8, 8, 64, 0, 300, "f16"),        # prefill from scratch, group 1
     ("bf16", 16, 8, 128, 1000, 77, "bf16"),  # group 2, ragged query block
-    ("f16", 64, 8, 128, 513, 40, "f32"),     # group 8, fp32 queries rounded to fp16
+    ("f16", 64, 8, 128, 513, 40, "f32"),     # group 8, fp32 queries as hi + lo fp16
     ("bf16", 32, 4, 64, 255, 129, "bf16"),   # head_dim 64, crosses page boundaries
     ("f16", 4, 4, 128, 7, 1, "f16"),         # single query
+    ("bf16", 32, 8, 128, 4000, 300, "f32"),  # fp32 queries as hi + lo bf16, two N tiles
+    ("bf16", 8, 2, 64, 130, 1000, "f16"),    # fp16 queries into a bf16 cache, four N tiles
+    ("f16", 16, 2, 128, 70000, 5, "f16"),    # few queries over a long cache: split-K, 3 stages
 ])
 def test_chunk_mfma_shapes(gpu, dtype, heads, kv_heads, D, pos0, nq, q_dtype):
     n = pos0 + nq
     Kb, Kd, Vb, Vd = make(n + heads, n, kv_heads * D, dtype)
     qb, qd = to_dtype_bits(np.random.default_rng(n).standard_normal((nq, heads * D), dtype=np.float32), q_dtype)
-    if q_dtype == "f32":  # the MFMA path takes fp16 queries: compare against that rounding
-        qd = qd.astype(np.float16).astype(np.float32)
     scale = 1 / math.sqrt(D)
     with qr.PagedKvCache(1, heads, kv_heads, D, n + 10, kv_dtype=dtype) as kv:
         kv.AppendRange(0, 0, Kb, Vb, src_dtype=dtype)
