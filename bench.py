@@ -55,6 +55,9 @@ WORKLOADS = {
     "c3-prefill": dict(kind="chunk", heads=32, kv=8, D=128, n=6144, dtype="bf16", B=1, rope=0.0, nq=2048,
                        q_dtype="bf16",
                        desc="llama-3-8b-shape chunked prefill, 2048 causal bf16 queries after 6144 cached tokens"),
+    "f1-rope-append": dict(kind="rope", heads=32, kv=8, D=128, n=2048, pos0=6144, dtype="f16", B=1, rope=500000.0,
+                           desc="fused RoPE + append of 2048 positions (8B shape: 32 q heads, 8 kv heads, "
+                                "head_dim 128) into an fp16 cache at positions 6144..8191"),
     "c5-mla": dict(kind="mla", heads=128, kv_lora=512, rope_dim=64, n=16384, dtype="bf16", B=1,
                    desc="MLA absorbed decode, 128 heads, 512+64 latent, 16384 cached bf16 tokens"),
 }
@@ -85,6 +88,12 @@ def algorithmic(w):
         pages = math.ceil(w["n"] / 256)
         b = w["n"] * width * esize(w["dtype"]) + w["heads"] * width * 4 + w["heads"] * w["kv_lora"] * 4 + pages * 4
         f = 2 * w["heads"] * w["n"] * (width + w["kv_lora"])
+        return b, f
+    if w["kind"] == "rope":
+        # read q, k, v (fp32), write q (fp32) and k, v (cache dtype); 6 flops per rotated pair
+        n, kvd, qd = w["n"], w["kv"] * w["D"], w["heads"] * w["D"]
+        b = n * (2 * qd * 4 + 2 * kvd * 4 + 2 * kvd * esize(w["dtype"])) + math.ceil(n / 256) * 4
+        f = n * (qd + kvd) // 2 * 6
         return b, f
     nq = w.get("nq", 1)
     total = w["n"] + (nq if w["kind"] == "chunk" else 0)
@@ -179,6 +188,20 @@ def run_gpu(w, steps, warmup):
             r = i % R
             cache.AbsorbedAttentionDev(r, w["n"] - 1, qt[r], qrp[r], u[r], scale, stream=stream)
         handle = cache
+    elif w["kind"] == "rope":
+        n, kvd, qd = w["n"], w["kv"] * w["D"], w["heads"] * w["D"]
+        set_bytes = n * (qd + 2 * kvd) * 4
+        R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
+        kv = qr.PagedKvCache(1, w["heads"], w["kv"], w["D"], w["pos0"] + n, kv_dtype=w["dtype"], max_batch=R)
+        kv.Reserve(R * math.ceil((w["pos0"] + n) / 256))
+        qs = torch.randn(R, n, qd, device=dev, generator=gen)
+        ks = torch.randn(R, n, kvd, device=dev, generator=gen)
+        vs = torch.randn(R, n, kvd, device=dev, generator=gen)
+
+        def step(i):
+            r = i % R
+            kv.AppendRopeDev(0, w["pos0"], qs[r], ks[r], vs[r], w["rope"], seq_id=r, stream=stream)
+        handle = kv
     else:
         kv, R = build_decode(w, gen, dev)
         B = w["B"]
@@ -217,7 +240,7 @@ def run_gpu(w, steps, warmup):
     wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1) / steps
     kernel_ms = None
-    if hasattr(handle, "SetSplitEvent"):
+    if hasattr(handle, "SetSplitEvent") and w["kind"] != "rope":
         kernel_ms = time_split_kernel(handle, step, warmup + steps, steps, stream)
     handle.close()
     return ms, wall * 1e3 / steps, kernel_ms
@@ -272,7 +295,23 @@ def cpu_baseline(w, budget_s=10.0):
         pass
     rng = np.random.default_rng(7)
     bytes_step, _ = algorithmic(w)
-    if w["kind"] == "mla":
+    if w["kind"] == "rope":
+        sample_rows = 64
+        qd, kvd = w["heads"] * w["D"], w["kv"] * w["D"]
+        Q = rng.standard_normal((sample_rows, qd), dtype=np.float32)
+        K = rng.standard_normal((sample_rows, kvd), dtype=np.float32)
+        V = rng.standard_normal((sample_rows, kvd), dtype=np.float32)
+        pages = np.zeros((2, sample_rows, kvd), np.float32)
+
+        def call():  # BuildCosSin + Rope on q and k, then the row copies of Append
+            qr_ = oracle.rope_rows(Q, w["D"], w["pos0"], w["rope"])
+            kr = oracle.rope_rows(K, w["D"], w["pos0"], w["rope"])
+            pages[0] = kr
+            pages[1] = V
+            return qr_
+        unit_fraction = sample_rows / w["n"]
+        sample = f"{sample_rows} of {w['n']} positions, fp32 storage"
+    elif w["kind"] == "mla":
         width = w["kv_lora"] + w["rope_dim"]
         lat = rng.standard_normal((w["n"], width), dtype=np.float32)
         qt = rng.standard_normal((w["heads"], w["kv_lora"]), dtype=np.float32)

@@ -96,6 +96,21 @@ int qr_kv_append_range(qr_kv* kv, int seq_id, int layer, int pos0, int n, const 
 int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k_dev,
                            const void* v_dev, int src_dtype, void* stream);
 
+/* Replaces the RoPE + Append step of StreamingEngine.Forward
+ * (StreamingEngine.cs:245-248; TransformerOps.BuildCosSinInto / Rope, TransformerOps.cs:56-88;
+ * PagedKvCache.Append, PagedKvCache.cs:62-69) for one position: the kv_dim-float k row
+ * and the heads*head_dim q row are rotated in place in the reference's rotate-half
+ * convention with cos/sin of pos * theta^(-2i/head_dim); the rotated k and the v row
+ * are appended at pos, and the rotated q is written back to `q` (the reference rotates
+ * pq in place before Attention).  k and v must be full kv_dim rows. */
+int qr_kv_append_rope(qr_kv* kv, int seq_id, int layer, int pos, float* q, const float* k,
+                      const float* v, float theta);
+/* Same for n consecutive positions pos0..pos0+n-1 with device rows: q_dev
+ * [n][heads*head_dim] (rotated in place; may be null), k_dev and v_dev [n][kv_dim] fp32,
+ * each 16-byte aligned; enqueued on `stream`. */
+int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q_dev,
+                          const float* k_dev, const float* v_dev, float theta, void* stream);
+
 /* Attention(layer, pos, q, attn, scale), PagedKvCache.cs:83-136:
  * attn[h*D:(h+1)*D] = softmax(q_h . K[0..pos, kvh(h)] * scale) . V[0..pos, kvh(h)],
  * kvh(h) = h*kv_heads/heads.  q and attn are host fp32 [heads*head_dim]. */

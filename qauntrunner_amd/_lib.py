@@ -72,6 +72,8 @@ SIGNATURES = {
     "qr_kv_append": [_p, _i, _i, _i, _p, _i, _p, _i],
     "qr_kv_append_range": [_p, _i, _i, _i, _i, _p, _p, _i],
     "qr_kv_append_range_dev": [_p, _i, _i, _i, _i, _p, _p, _i, _p],
+    "qr_kv_append_rope": [_p, _i, _i, _i, _p, _p, _p, _f],
+    "qr_kv_append_rope_dev": [_p, _i, _i, _i, _i, _p, _p, _p, _f, _p],
     "qr_kv_attention": [_p, _i, _i, _i, _p, _p, _f],
     "qr_kv_attention_batch": [_p, _i, _p, _i, _p, _p, _p, _f],
     "qr_kv_attention_dev": [_p, _i, _p, _i, _p, _p, _p, _f, _p],

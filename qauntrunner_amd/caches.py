@@ -131,6 +131,24 @@ class PagedKvCache:
                                                ctypes.c_void_p(v_rows.data_ptr()), dtype_code(src_dtype),
                                                _stream_ptr(stream)))
 
+    def AppendRope(self, layer, pos, q, k, v, theta, seq_id=0) -> np.ndarray:
+        """StreamingEngine.cs:245-248: RoPE on q and k at `pos` (TransformerOps.cs:56-88),
+        then Append(k, v).  Returns the rotated q (the reference rotates it in place)."""
+        q = np.array(q, dtype=np.float32, copy=True).reshape(-1)
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        if q.size != self.Heads * self.HeadDim or k.size != self.KvDim or v.size != self.KvDim:
+            raise ValueError("q must be heads*head_dim floats, k and v kv_dim floats")
+        check(self._lib.qr_kv_append_rope(self._h, seq_id, layer, pos, _ptr(q), _ptr(k), _ptr(v), theta))
+        return q
+
+    def AppendRopeDev(self, layer, pos0, q_rows, k_rows, v_rows, theta, seq_id=0, stream=None) -> None:
+        """n positions from device rows; q_rows (or None) is rotated in place."""
+        n = k_rows.numel() // self.KvDim
+        qp = ctypes.c_void_p(q_rows.data_ptr()) if q_rows is not None else ctypes.c_void_p()
+        check(self._lib.qr_kv_append_rope_dev(self._h, seq_id, layer, pos0, n, qp, ctypes.c_void_p(k_rows.data_ptr()),
+                                              ctypes.c_void_p(v_rows.data_ptr()), theta, _stream_ptr(stream)))
+
     def Reset(self, seq_id=-1) -> None:  # PagedKvCache.cs:72
         check(self._lib.qr_kv_reset(self._h, seq_id))
 

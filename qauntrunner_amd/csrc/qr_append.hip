@@ -81,6 +81,94 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherArgs a) {
     }
 }
 
+// Workgroup = kRopeRows positions.  The cos/sin of (position, i) for i < head_dim/2 are
+// computed once into LDS; then every thread takes 4 consecutive dim pairs (d..d+3,
+// d+D/2..d+D/2+3) of one head: K heads are rotated and stored in the cache dtype with
+// the same dims of V, q heads are rotated in place.  Products and sums are separately
+// rounded as in the reference (x0 c - x1 s, x0 s + x1 c).
+constexpr int kRopeRows = 1;
+
+// 4 consecutive dims of one cache row: one 16- or 8-byte store when the plane is
+// token-major, element stores when it is dims-major.
+__device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g, long long phys, int plane, int kvh,
+                                       int slot, int d, const float (&x)[4]) {
+    const bool rows = !(plane == 1 && g.v_dims_major);
+    if (dtype == QR_DTYPE_F32 && rows) {
+        *reinterpret_cast<float4*>(static_cast<float*>(pool) + g.offset(phys, plane, kvh, slot, d)) =
+            make_float4(x[0], x[1], x[2], x[3]);
+        return;
+    }
+    uint16_t b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b[e] = dtype == QR_DTYPE_F16 ? f32_to_f16_bits_ref(x[e]) : f32_to_bf16_bits_ref(x[e]);
+    uint16_t* base = static_cast<uint16_t*>(pool);
+    if (rows) {
+        *reinterpret_cast<uint2*>(base + g.offset(phys, plane, kvh, slot, d)) =
+            make_uint2(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16));
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) base[g.offset(phys, plane, kvh, slot, d + e)] = b[e];
+}
+
+__global__ void __launch_bounds__(256) rope_append_kernel(const RopeAppendArgs a) {
+    const AppendArgs& g = a.app;
+    const int D = g.geom.head_dim;
+    const int half = D >> 1;
+    const int kv_heads = g.geom.kv_heads;
+    const int q_heads = a.q ? a.q_width / D : 0;
+    const int r0 = blockIdx.x * kRopeRows;
+    __shared__ float cs[kRopeRows][2][kMaxRopeHalf];
+    for (int idx = threadIdx.x; idx < kRopeRows * half; idx += 256) {
+        const int r = idx / half, i = idx - r * half;
+        const float ang = __fmul_rn(static_cast<float>(g.pos0 + r0 + r), a.freq[i]);
+        cs[r][0][i] = cosf(ang);
+        cs[r][1][i] = sinf(ang);
+    }
+    __syncthreads();
+    const int per_head = half / 4;
+    const int heads = kv_heads + q_heads;
+    for (int it = threadIdx.x; it < kRopeRows * heads * per_head; it += 256) {
+        const int r = it / (heads * per_head);
+        const int rem = it - r * heads * per_head;
+        const int h = rem / per_head;
+        const int d = 4 * (rem - h * per_head);
+        if (r0 + r >= g.n) continue;
+        const float4 c = *reinterpret_cast<const float4*>(&cs[r][0][d]);
+        const float4 sn = *reinterpret_cast<const float4*>(&cs[r][1][d]);
+        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
+        const long long row = r0 + r;
+        const float* src = h < kv_heads ? static_cast<const float*>(g.src[0]) + row * g.src_stride + h * D
+                                        : a.q + row * a.q_width + (h - kv_heads) * D;
+        const float4 a0 = *reinterpret_cast<const float4*>(src + d);
+        const float4 a1 = *reinterpret_cast<const float4*>(src + d + half);
+        const float x0[4] = {a0.x, a0.y, a0.z, a0.w}, x1[4] = {a1.x, a1.y, a1.z, a1.w};
+        float y0[4], y1[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            y0[e] = __fsub_rn(__fmul_rn(x0[e], cc[e]), __fmul_rn(x1[e], ss[e]));
+            y1[e] = __fadd_rn(__fmul_rn(x0[e], ss[e]), __fmul_rn(x1[e], cc[e]));
+        }
+        if (h < kv_heads) {
+            const int t = g.pos0 + r0 + r;
+            const long long phys = g.page_table[t >> kPageShift];
+            const int slot = t & (kPageTokens - 1);
+            store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d, y0);
+            store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d + half, y1);
+            const float* v = static_cast<const float*>(g.src[1]) + row * g.src_stride + h * D;
+            const float4 b0 = *reinterpret_cast<const float4*>(v + d);
+            const float4 b1 = *reinterpret_cast<const float4*>(v + d + half);
+            const float v0[4] = {b0.x, b0.y, b0.z, b0.w}, v1[4] = {b1.x, b1.y, b1.z, b1.w};
+            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d, v0);
+            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d + half, v1);
+        } else {
+            float* q = a.q + row * a.q_width + (h - kv_heads) * D;
+            *reinterpret_cast<float4*>(q + d) = make_float4(y0[0], y0[1], y0[2], y0[3]);
+            *reinterpret_cast<float4*>(q + d + half) = make_float4(y1[0], y1[1], y1[2], y1[3]);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) widen_kernel(const void* src, int dtype, float* dst, long long n) {
     for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += static_cast<long long>(gridDim.x) * 256)
         dst[i] = load_f32(src, dtype, i);
@@ -106,6 +194,12 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
     const long long total = static_cast<long long>(a.n) * a.geom.kv_heads * a.geom.head_dim * a.geom.planes;
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(gather_kernel, dim3(grid_for(total)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
+    if (a.app.n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_append_kernel, dim3((a.app.n + kRopeRows - 1) / kRopeRows), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

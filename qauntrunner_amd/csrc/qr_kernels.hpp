@@ -64,6 +64,20 @@ struct GatherArgs {
 };
 hipError_t launch_gather(const GatherArgs& a, hipStream_t stream);
 
+// Fused RoPE + append (StreamingEngine.cs:245-248): rows pos0..pos0+n-1 of fp32 K are
+// rotated (rotate-half, TransformerOps.cs:56-88) and, with V, converted to the cache
+// dtype and scattered into their pages; q rows of the same positions ([n][q_width],
+// q_width a multiple of head_dim) are rotated in place.  freq[i] = theta^(-2i/D) is
+// computed on the host with the same libm powf as the reference's MathF.Pow path.
+constexpr int kMaxRopeHalf = 128;  // head_dim <= 256
+struct RopeAppendArgs {
+    AppendArgs app;         // src[0] = K, src[1] = V, fp32, row length kv_dim
+    float* q;               // may be null
+    int q_width;
+    float freq[kMaxRopeHalf];
+};
+hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream);
+
 // Widens 16-bit rows to fp32 (exact) -- used for 16-bit query inputs.
 hipError_t launch_widen(const void* src, int src_dtype, float* dst, long long n, hipStream_t stream);
 

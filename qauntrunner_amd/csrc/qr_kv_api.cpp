@@ -1,5 +1,6 @@
 // qr_kv.cpp -- C ABI of the paged GQA KV cache (PagedKvCache, PagedKvCache.cs:12-136).
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -78,6 +79,35 @@ int append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k,
     a.pos0 = pos0;
     a.n = n;
     QR_HIP(launch_append(a, stream));
+    int& sl = kv->seq_len[seq_id];
+    sl = std::max(sl, pos0 + n);  // PagedKvCache.cs:68
+    return QR_OK;
+}
+
+// RoPE + append of n positions from device rows (fp32 k/v, q rotated in place).
+int rope_append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q, const float* k,
+                    const float* v, float theta, hipStream_t stream) {
+    QR_TRY(kv->store.ensure(seq_id, layer, pos0 + n, stream));
+    RopeAppendArgs a{};
+    a.app.pool = kv->store.pool();
+    a.app.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+    a.app.geom = kv->store.geom();
+    a.app.dtype = kv->dtype;
+    a.app.src[0] = k;
+    a.app.src[1] = v;
+    a.app.row_len[0] = kv->kv_dim;
+    a.app.row_len[1] = kv->kv_dim;
+    a.app.src_stride = kv->kv_dim;
+    a.app.src_dtype = QR_DTYPE_F32;
+    a.app.pos0 = pos0;
+    a.app.n = n;
+    a.q = q;
+    a.q_width = kv->heads * kv->head_dim;
+    // freq_i = theta^(-2i/D) with the host libm powf, in the reference's fp32 order
+    // (TransformerOps.cs:60: MathF.Pow(theta, -2f * i / headDim))
+    const int half = kv->head_dim / 2;
+    for (int i = 0; i < half; ++i) a.freq[i] = std::pow(theta, (-2.0f * static_cast<float>(i)) / static_cast<float>(kv->head_dim));
+    QR_HIP(launch_rope_append(a, stream));
     int& sl = kv->seq_len[seq_id];
     sl = std::max(sl, pos0 + n);  // PagedKvCache.cs:68
     return QR_OK;
@@ -273,6 +303,46 @@ int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, co
     DeviceGuard dg(kv->device);
     return append_dev(kv, seq_id, layer, pos0, n, k_dev, v_dev, kv->kv_dim, kv->kv_dim, src_dtype,
                       as_stream(stream));
+}
+
+int qr_kv_append_rope(qr_kv* kv, int seq_id, int layer, int pos, float* q, const float* k, const float* v,
+                      float theta) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_TRY(check_pos(kv, pos));
+    QR_CHECK_ARG(q && k && v, "null q/k/v row");
+    DeviceGuard dg(kv->device);
+    const size_t kbytes = static_cast<size_t>(kv->kv_dim) * 4;
+    const size_t qbytes = static_cast<size_t>(kv->heads) * kv->head_dim * 4;
+    QR_TRY(kv->stage.ensure(2 * kbytes + qbytes + 512));
+    char* st = static_cast<char*>(kv->stage.get());
+    float* dk = reinterpret_cast<float*>(st);
+    float* dv = reinterpret_cast<float*>(st + kbytes);
+    float* dq = reinterpret_cast<float*>(st + 2 * kbytes);
+    QR_HIP(hipMemcpyAsync(dk, k, kbytes, hipMemcpyHostToDevice, kv->stream));
+    QR_HIP(hipMemcpyAsync(dv, v, kbytes, hipMemcpyHostToDevice, kv->stream));
+    QR_HIP(hipMemcpyAsync(dq, q, qbytes, hipMemcpyHostToDevice, kv->stream));
+    QR_TRY(rope_append_dev(kv, seq_id, layer, pos, 1, dq, dk, dv, theta, kv->stream));
+    QR_HIP(hipMemcpyAsync(q, dq, qbytes, hipMemcpyDeviceToHost, kv->stream));
+    QR_HIP(hipStreamSynchronize(kv->stream));
+    return QR_OK;
+}
+
+int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q_dev, const float* k_dev,
+                          const float* v_dev, float theta, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(n >= 0, "negative row count %d", n);
+    QR_CHECK_ARG(n == 0 || (k_dev && v_dev), "null k/v rows");
+    if (n == 0) return QR_OK;
+    QR_TRY(check_pos(kv, pos0));
+    QR_TRY(check_pos(kv, pos0 + n - 1));
+    QR_CHECK_ARG(((reinterpret_cast<uintptr_t>(q_dev) | reinterpret_cast<uintptr_t>(k_dev) |
+                   reinterpret_cast<uintptr_t>(v_dev)) & 15) == 0, "q/k/v rows must be 16-byte aligned");
+    DeviceGuard dg(kv->device);
+    return rope_append_dev(kv, seq_id, layer, pos0, n, q_dev, k_dev, v_dev, theta, as_stream(stream));
 }
 
 int qr_kv_attention(qr_kv* kv, int seq_id, int layer, int pos, const float* q, float* attn, float scale) {
