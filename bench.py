@@ -60,7 +60,21 @@ WORKLOADS = {
                                 "head_dim 128) into an fp16 cache at positions 6144..8191"),
     "c5-mla": dict(kind="mla", heads=128, kv_lora=512, rope_dim=64, n=16384, dtype="bf16", B=1,
                    desc="MLA absorbed decode, 128 heads, 512+64 latent, 16384 cached bf16 tokens"),
+    "f2-mla-layer": dict(kind="mla_layer", heads=128, kv_lora=512, rope_dim=64, nope=128, vdim=128, n=16384,
+                         dtype="bf16", kvb_fmt="BF16", B=1,
+                         desc="MLA absorbed layer block for one token: q-absorb through bf16 W_UK, attention over "
+                              "16384 cached bf16 latents (128 heads, 512+64), W_UV up-projection (nope 128, v 128)"),
+    "f2-mla-layer-q8": dict(kind="mla_layer", heads=128, kv_lora=512, rope_dim=64, nope=128, vdim=128, n=16384,
+                            dtype="bf16", kvb_fmt="Q8_0", B=1,
+                            desc="MLA absorbed layer block as f2-mla-layer with the kvb weights in Q8_0"),
 }
+
+KVB_FORMATS = {"F32": (0, 1, 4), "F16": (1, 1, 2), "BF16": (2, 1, 2), "Q8_0": (4, 32, 34)}  # code, block, bytes
+
+
+def kvb_bytes(w):
+    code, bs, bb = KVB_FORMATS[w["kvb_fmt"]]
+    return w["heads"] * (w["nope"] + w["vdim"]) * (w["kv_lora"] // bs * bb)
 
 
 def profiled_traffic(name):
@@ -88,6 +102,15 @@ def algorithmic(w):
         pages = math.ceil(w["n"] / 256)
         b = w["n"] * width * esize(w["dtype"]) + w["heads"] * width * 4 + w["heads"] * w["kv_lora"] * 4 + pages * 4
         f = 2 * w["heads"] * w["n"] * (width + w["kv_lora"])
+        return b, f
+    if w["kind"] == "mla_layer":
+        # latents + every kvb row once + q in + out; the q~/u hand-offs between kernels are not counted
+        width = w["kv_lora"] + w["rope_dim"]
+        pages = math.ceil(w["n"] / 256)
+        H, nope, vdim, L = w["heads"], w["nope"], w["vdim"], w["kv_lora"]
+        b = (w["n"] * width * esize(w["dtype"]) + kvb_bytes(w) + H * (nope + w["rope_dim"]) * 4 + H * vdim * 4
+             + pages * 4)
+        f = 2 * H * w["n"] * (width + L) + 2 * H * (nope + vdim) * L
         return b, f
     if w["kind"] == "rope":
         # read q, k, v (fp32), write q (fp32) and k, v (cache dtype); 6 flops per rotated pair
@@ -188,6 +211,31 @@ def run_gpu(w, steps, warmup):
             r = i % R
             cache.AbsorbedAttentionDev(r, w["n"] - 1, qt[r], qrp[r], u[r], scale, stream=stream)
         handle = cache
+    elif w["kind"] == "mla_layer":
+        width = w["kv_lora"] + w["rope_dim"]
+        H, nope, vdim, L = w["heads"], w["nope"], w["vdim"], w["kv_lora"]
+        code = KVB_FORMATS[w["kvb_fmt"]][0]
+        set_bytes = w["n"] * width * esize(w["dtype"]) + kvb_bytes(w)
+        R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
+        cache = qr.MlaLatentCache(R, L, w["rope_dim"], w["n"], dtype=w["dtype"])
+        cache.Reserve(R * math.ceil(w["n"] / 256))
+        kvbs = []
+        for layer in range(R):
+            rows = torch.randn(w["n"], width, device=dev, generator=gen)
+            cache.AppendRangeDev(layer, 0, to_cache_bits(rows, w["dtype"]), src_dtype=w["dtype"])
+            kvbs.append(synth_kvb(w, gen, dev))
+        q = torch.randn(R, H, nope + w["rope_dim"], device=dev, generator=gen)
+        out = torch.empty(R, H, vdim, device=dev)
+
+        def step(i):
+            r = i % R
+            cache.AttendAbsorbedDev(r, w["n"] - 1, q[r], kvbs[r], code, nope, vdim, out[r], stream=stream)
+        handle = cache
+        proj = {"absorb": lambda r: qr.mla_q_absorb_dev(kvbs[r], code, H, nope, w["rope_dim"], vdim, L, q[r],
+                                                        qt_scratch[r], stream=stream),
+                "wuv": lambda r: qr.mla_wuv_dev(kvbs[r], code, H, nope, vdim, L, qt_scratch[r], out[r],
+                                                stream=stream)}
+        qt_scratch = torch.randn(R, H, L, device=dev, generator=gen)
     elif w["kind"] == "rope":
         n, kvd, qd = w["n"], w["kv"] * w["D"], w["heads"] * w["D"]
         set_bytes = n * (qd + 2 * kvd) * 4
@@ -242,8 +290,40 @@ def run_gpu(w, steps, warmup):
     kernel_ms = None
     if hasattr(handle, "SetSplitEvent") and w["kind"] != "rope":
         kernel_ms = time_split_kernel(handle, step, warmup + steps, steps, stream)
+    extra = None
+    if w["kind"] == "mla_layer":
+        extra = {}
+        for name, fn in proj.items():
+            for i in range(warmup):
+                fn(i % R)
+            t0.record(stream)
+            for i in range(steps):
+                fn((warmup + i) % R)
+            t1.record(stream)
+            torch.cuda.synchronize()
+            extra[name] = t0.elapsed_time(t1) / steps
     handle.close()
-    return ms, wall * 1e3 / steps, kernel_ms
+    return ms, wall * 1e3 / steps, kernel_ms, extra
+
+
+def synth_kvb(w, gen, dev):
+    """kvb rows [heads*(nope+vdim)][kv_lora] in the workload's format, N(0, 0.05^2) weights
+    (Q8_0: random int8 values under an f16 scale of 0.05/127), as a uint8 device tensor."""
+    import torch
+
+    rows = w["heads"] * (w["nope"] + w["vdim"])
+    L = w["kv_lora"]
+    fmt = w["kvb_fmt"]
+    if fmt == "Q8_0":
+        blocks = rows * L // 32
+        raw = torch.randint(0, 256, (blocks, 34), dtype=torch.uint8, device=dev, generator=gen)
+        d = torch.full((blocks,), 0.05 / 127, dtype=torch.float16, device=dev)
+        raw[:, 0:2] = d.view(torch.uint8).view(blocks, 2)
+        return raw.reshape(-1)
+    x = torch.randn(rows, L, device=dev, generator=gen) * 0.05
+    if fmt == "F32":
+        return x.view(torch.uint8).reshape(-1)
+    return to_cache_bits(x, "f16" if fmt == "F16" else "bf16").view(torch.uint8).reshape(-1)
 
 
 def time_split_kernel(handle, step, first, steps, stream):
@@ -311,6 +391,22 @@ def cpu_baseline(w, budget_s=10.0):
             return qr_
         unit_fraction = sample_rows / w["n"]
         sample = f"{sample_rows} of {w['n']} positions, fp32 storage"
+    elif w["kind"] == "mla_layer":
+        width = w["kv_lora"] + w["rope_dim"]
+        H, nope, vdim, L, rp = w["heads"], w["nope"], w["vdim"], w["kv_lora"], w["rope_dim"]
+        heads_sample = 4
+        lat = rng.standard_normal((w["n"], width), dtype=np.float32)
+        kvb = (rng.standard_normal((heads_sample * (nope + vdim), L), dtype=np.float32) * 0.05)
+        q = rng.standard_normal((heads_sample, nope + rp), dtype=np.float32)
+        scale = 1 / math.sqrt(nope + rp)
+
+        def call():  # absorb, attention, W_UV for a sample of heads (kvb already decoded)
+            qt = oracle.mla_q_absorb(q, kvb, heads_sample, nope, rp, vdim, L)
+            u = oracle.mla_attention(lat, qt, q[:, nope:], L, rp, scale)
+            return oracle.mla_wuv(u, kvb, heads_sample, nope, vdim, L)
+        unit_fraction = heads_sample / H
+        sample = (f"absorb + attention over {w['n']} tokens + W_UV for {heads_sample} of {H} heads, "
+                  "scaled to all heads, kvb pre-decoded to fp32")
     elif w["kind"] == "mla":
         width = w["kv_lora"] + w["rope_dim"]
         lat = rng.standard_normal((w["n"], width), dtype=np.float32)
@@ -381,7 +477,7 @@ def main():
         sys.exit(2)
 
     w = WORKLOADS[args.config]
-    ms, wall_ms, kernel_ms = run_gpu(w, args.steps, args.warmup)
+    ms, wall_ms, kernel_ms, extra = run_gpu(w, args.steps, args.warmup)
     bytes_step, flops_step = algorithmic(w)
     tbs = bytes_step / (ms * 1e-3) / 1e12
     kms = kernel_ms if kernel_ms else ms  # dominant kernel's average duration
@@ -418,6 +514,17 @@ def main():
                    "algorithmic_flops": flops_step, "host_wall_ms_per_step": round(wall_ms, 4)},
         "roofline": roof,
     }
+    if extra:
+        # the projection kernels timed alone (HIP events around `steps` launches each)
+        H, nope, vdim, L = w["heads"], w["nope"], w["vdim"], w["kv_lora"]
+        per_row = kvb_bytes(w) // (H * (nope + vdim))
+        proj_bytes = {"absorb": H * nope * per_row + H * (nope + w["rope_dim"]) * 4 + H * L * 4,
+                      "wuv": H * vdim * per_row + H * L * 4 + H * vdim * 4}
+        line["projections"] = {
+            k: {"kernel_us": round(v * 1e3, 3), "algorithmic_bytes": proj_bytes[k],
+                "achieved_GBs": round(proj_bytes[k] / (v * 1e-3) / 1e9, 1),
+                "frac": round(proj_bytes[k] / (v * 1e-3) / 1e9 / (HBM_PEAK_TBS * 1e3), 4)}
+            for k, v in extra.items()}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -44,6 +44,18 @@ enum {
     QR_DTYPE_BF16 = 2
 };
 
+/* weight-row formats: QuantFormat values, Dtypes.cs:6-26 (block specs :38-50).
+ * The F32/F16/BF16 codes coincide with QR_DTYPE_*. */
+enum {
+    QR_FMT_F32 = 0,  /* 4 B / weight                                     */
+    QR_FMT_F16 = 1,  /* 2 B / weight                                     */
+    QR_FMT_BF16 = 2, /* 2 B / weight                                     */
+    QR_FMT_Q4_0 = 3, /* 32 weights / 20 B: f16 d, 16 nibble bytes, 2 pad */
+    QR_FMT_Q8_0 = 4, /* 32 weights / 34 B: f16 d, 32 int8                */
+    QR_FMT_Q4_K = 6, /* 256 weights / 144 B                              */
+    QR_FMT_Q6_K = 7  /* 256 weights / 210 B                              */
+};
+
 /* status codes */
 enum {
     QR_OK = 0,
@@ -56,6 +68,7 @@ enum {
 
 typedef struct qr_kv qr_kv;   /* PagedKvCache  */
 typedef struct qr_mla qr_mla; /* MlaLatentCache */
+typedef struct qr_weight qr_weight; /* one HBM-resident weight tensor (a ModelStore view) */
 
 /* ---- library ---------------------------------------------------------- */
 int qr_abi_version(void);
@@ -185,6 +198,20 @@ int qr_mla_attention(qr_mla* mla, int layer, int pos, int heads, const float* q_
                      const float* q_rope, float scale, float* u);
 int qr_mla_attention_dev(qr_mla* mla, int layer, int pos, int heads, const float* q_tilde_dev,
                          const float* q_rope_dev, float scale, float* u_dev, void* stream);
+/* The whole absorbed block of MlaLayer after cache.Append, StreamingEngine.cs:508-577:
+ *   q~_h = sum_{j<nope} q_h[j] * W_kvb[h*(nope+vdim)+j]          (:517-529)
+ *   u_h  = absorbed attention over positions 0..pos, scale 1/sqrt(nope+rope) (:511, :531-568)
+ *   out_h[j] = DotF32(W_kvb[h*(nope+vdim)+nope+j], u_h)         (:569-576)
+ * q [heads][nope+rope] fp32 (rope part already rotated, :499-501), out [heads][vdim].
+ * kvb: [heads*(nope+vdim)][kv_lora] weights (qr_weight_create), decoded on the fly
+ * exactly as BlockDequantizer.Dequantize; kv_lora a multiple of 8 and of the format's
+ * block.  The projections reproduce the reference's fp32 operation order bit for bit. */
+int qr_mla_attend_absorbed(qr_mla* mla, int layer, int pos, int heads, int nope, int vdim,
+                           const float* q, const qr_weight* kvb, float* out);
+/* Same on device buffers: kvb_dev 16-byte aligned, q_dev/out_dev 8-byte aligned. */
+int qr_mla_attend_absorbed_dev(qr_mla* mla, int layer, int pos, int heads, int nope, int vdim,
+                               const float* q_dev, const void* kvb_dev, int kvb_format,
+                               float* out_dev, void* stream);
 int qr_mla_reset(qr_mla* mla);                    /* MlaLatentCache.cs:53 */
 int qr_mla_truncate(qr_mla* mla, int len);        /* MlaLatentCache.cs:57 */
 int qr_mla_seq_len(const qr_mla* mla, int* out);  /* MlaLatentCache.cs:19 */
@@ -193,6 +220,27 @@ int qr_mla_page_count(const qr_mla* mla, int layer, int* out); /* MlaLatentCache
 /* Page(layer, page), MlaLatentCache.cs:63: copies one page out as fp32
  * [256][latentDim] (16-bit caches decoded exactly). */
 int qr_mla_read_page(qr_mla* mla, int layer, int page, float* out);
+
+/* ---- weights and MLA projections -------------------------------------- */
+
+/* Bytes of one row of `cols` weights (Dtypes.TensorBytes, Dtypes.cs:38-60). */
+int qr_weight_row_bytes(int format, int cols, long long* out);
+/* Uploads one weight tensor (rows x cols, rows back to back in `format`) into HBM on
+ * the current device: the ModelStore view a layer reads (ModelStore.cs, RowPtr/RowBytes). */
+int qr_weight_create(qr_weight** out, int format, long long rows, int cols, const void* host_bytes);
+int qr_weight_destroy(qr_weight* w);
+int qr_weight_data(const qr_weight* w, const void** dev_ptr);
+/* q-absorb, StreamingEngine.cs:517-529, for nq query rows:
+ *   q_tilde[b][h][k] = (((0 + q[b][h][0]*W[h*(nope+vdim)+0][k]) + q[b][h][1]*W[..+1][k]) + ...)
+ * rows dequantized as BlockDequantizer.Dequantize (:524-526).  q_dev [nq][heads][nope+rope],
+ * q_tilde_dev [nq][heads][kv_lora] (8-byte aligned), kvb_dev 16-byte aligned. */
+int qr_mla_q_absorb_dev(const void* kvb_dev, int kvb_format, int heads, int nope, int rope, int vdim,
+                        int kv_lora, int nq, const float* q_dev, float* q_tilde_dev, void* stream);
+/* W_UV, StreamingEngine.cs:569-576: out[b][h][j] = DotF32(W[h*(nope+vdim)+nope+j], u[b][h])
+ * with SimdMath.DotF32's lane order.  u_dev [nq][heads][kv_lora] (8-byte aligned),
+ * out_dev [nq][heads][vdim]. */
+int qr_mla_wuv_dev(const void* kvb_dev, int kvb_format, int heads, int nope, int vdim, int kv_lora,
+                   int nq, const float* u_dev, float* out_dev, void* stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,7 @@ _lib = None
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 _i, _l, _f, _d = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double
 
 
@@ -55,6 +56,8 @@ def lib():
             "qro_mla_q_absorb": (None, [_f32p, _f32p, _i, _i, _i, _i, _i, _f32p]),
             "qro_mla_wuv": (None, [_f32p, _f32p, _i, _i, _i, _i, _f32p]),
             "qro_mla_expanded_f64": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i, _i, _i, _d, _f64p]),
+            "qro_row_bytes": (ctypes.c_long, [_i, _l]),
+            "qro_dequant_row": (ctypes.c_int, [_i, _u8p, _l, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -195,4 +198,27 @@ def mla_expanded_f64(q, kvb, lat, heads, nope, rope, vdim, kv_lora, scale):
     out = np.empty((heads, vdim), np.float64)
     lib().qro_mla_expanded_f64(q.reshape(-1), kvb.reshape(-1), lat.reshape(-1), lat.shape[0],
                                heads, nope, rope, vdim, kv_lora, scale, out.reshape(-1))
+    return out
+
+
+# QuantFormat values (Dtypes.cs:6-26) that the decoders cover.
+FMT = {"F32": 0, "F16": 1, "BF16": 2, "Q4_0": 3, "Q8_0": 4, "Q4_K": 6, "Q6_K": 7}
+
+
+def row_bytes(fmt, n):
+    """Bytes of one row of n weights (Dtypes.cs:38-50); ValueError if not whole blocks."""
+    r = lib().qro_row_bytes(int(fmt), int(n))
+    if r < 0:
+        raise ValueError(f"format {fmt} cannot hold a row of {n} weights")
+    return r
+
+
+def dequant_rows(fmt, raw, n):
+    """BlockDequantizer.Dequantize on every row of raw (uint8 [rows][row_bytes]) -> fp32 [rows][n]."""
+    rb = row_bytes(fmt, n)
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, rb)
+    out = np.empty((raw.shape[0], n), np.float32)
+    for r in range(raw.shape[0]):
+        if lib().qro_dequant_row(int(fmt), raw[r], n, out[r]) != 0:
+            raise ValueError(f"format {fmt} unsupported")
     return out

@@ -387,3 +387,111 @@ void qro_mla_expanded_f64(const float* q, const float* kvb, const float* lat, in
     }
     free(s);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Weight-row decoders: Core/Quantization/BlockDequantizer.cs                */
+/* ------------------------------------------------------------------------- */
+
+/* Dtypes.cs:38-50: (weights per block, bytes per block). */
+static int fmt_spec(int fmt, int* bs, int* bb)
+{
+    switch (fmt) {
+    case 0: *bs = 1; *bb = 4; return 0;     /* F32  */
+    case 1: *bs = 1; *bb = 2; return 0;     /* F16  */
+    case 2: *bs = 1; *bb = 2; return 0;     /* BF16 */
+    case 3: *bs = 32; *bb = 20; return 0;   /* Q4_0: f16 d, 16 nibble bytes, 2 pad bytes */
+    case 4: *bs = 32; *bb = 34; return 0;   /* Q8_0: f16 d, 32 int8 */
+    case 6: *bs = 256; *bb = 144; return 0; /* Q4_K */
+    case 7: *bs = 256; *bb = 210; return 0; /* Q6_K */
+    default: return -1;
+    }
+}
+
+long qro_row_bytes(int fmt, long n)
+{
+    int bs, bb;
+    if (fmt_spec(fmt, &bs, &bb) || n < 0 || n % bs) return -1;
+    return n / bs * bb;
+}
+
+static inline uint16_t le16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* BlockDequantizer.cs:155-166 (ggml get_scale_min_k4): 6-bit scale and min of sub-block j. */
+static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+int qro_dequant_row(int fmt, const uint8_t* s, long n, float* y)
+{
+    if (qro_row_bytes(fmt, n) < 0) return -1;
+    switch (fmt) {
+    case 0: /* BlockDequantizer.cs:14 */
+        memcpy(y, s, (size_t)n * 4);
+        return 0;
+    case 1: /* :34-41 */
+        for (long i = 0; i < n; i++) y[i] = qro_f16_to_f32(le16(s + 2 * i));
+        return 0;
+    case 2: /* :43-50 */
+        for (long i = 0; i < n; i++) y[i] = qro_bf16_to_f32(le16(s + 2 * i));
+        return 0;
+    case 3: /* :52-69: low nibble -> weight i, high nibble -> weight i+16 */
+        for (long b = 0; b < n / 32; b++, s += 20, y += 32) {
+            float d = qro_f16_to_f32(le16(s));
+            for (int i = 0; i < 16; i++) {
+                y[i] = d * (float)((s[2 + i] & 0xF) - 8);
+                y[i + 16] = d * (float)((s[2 + i] >> 4) - 8);
+            }
+        }
+        return 0;
+    case 4: /* :71-84 */
+        for (long b = 0; b < n / 32; b++, s += 34, y += 32) {
+            float d = qro_f16_to_f32(le16(s));
+            for (int i = 0; i < 32; i++) y[i] = d * (float)(int8_t)s[2 + i];
+        }
+        return 0;
+    case 6: /* :168-196: d @0, dmin @2, packed scales @4, nibbles @16 (sub-block pairs share 32 bytes) */
+        for (long b = 0; b < n / 256; b++, s += 144, y += 256) {
+            float d = qro_f16_to_f32(le16(s)), dmin = qro_f16_to_f32(le16(s + 2));
+            for (int sub = 0; sub < 8; sub++) {
+                int sc, mi;
+                scale_min_k4(sub, s + 4, &sc, &mi);
+                float a = d * (float)sc, m = dmin * (float)mi;
+                const uint8_t* qb = s + 16 + (sub / 2) * 32;
+                for (int i = 0; i < 32; i++) {
+                    int qv = (sub & 1) ? (qb[i] >> 4) : (qb[i] & 0xF);
+                    float t = a * (float)qv;
+                    y[sub * 32 + i] = t - m;
+                }
+            }
+        }
+        return 0;
+    case 7: /* :228-256: ql @0, qh @128, int8 scales @192, d @208 */
+        for (long b = 0; b < n / 256; b++, s += 210, y += 256) {
+            float d = qro_f16_to_f32(le16(s + 208));
+            const uint8_t *ql = s, *qh = s + 128, *sc = s + 192;
+            for (int h = 0; h < 256; h += 128) {
+                for (int l = 0; l < 32; l++) {
+                    int is = l / 16;
+                    int q1 = (ql[h / 2 + l] & 0xF) | (((qh[h / 4 + l] >> 0) & 3) << 4);
+                    int q2 = (ql[h / 2 + l + 32] & 0xF) | (((qh[h / 4 + l] >> 2) & 3) << 4);
+                    int q3 = (ql[h / 2 + l] >> 4) | (((qh[h / 4 + l] >> 4) & 3) << 4);
+                    int q4 = (ql[h / 2 + l + 32] >> 4) | (((qh[h / 4 + l] >> 6) & 3) << 4);
+                    const int8_t* scs = (const int8_t*)sc + 8 * (h / 128) + is;
+                    y[h + l] = (d * (float)scs[0]) * (float)(q1 - 32);
+                    y[h + l + 32] = (d * (float)scs[2]) * (float)(q2 - 32);
+                    y[h + l + 64] = (d * (float)scs[4]) * (float)(q3 - 32);
+                    y[h + l + 96] = (d * (float)scs[6]) * (float)(q4 - 32);
+                }
+            }
+        }
+        return 0;
+    }
+    return -1;
+}

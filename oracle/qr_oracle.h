@@ -73,6 +73,15 @@ void qro_mla_wuv(const float* u, const float* kvb, int heads, int nope, int vdim
 void qro_mla_expanded_f64(const float* q, const float* kvb, const float* lat, int seq, int heads,
                           int nope, int rope, int vdim, int kv_lora, double scale, double* out);
 
+/* ---- weight rows: Core/Quantization/BlockDequantizer.cs ----
+ * fmt is a QuantFormat value (Dtypes.cs:6-26).  Supported here: F32 0, F16 1,
+ * BF16 2, Q4_0 3, Q8_0 4, Q4_K 6, Q6_K 7.
+ * qro_row_bytes: bytes of n weights (Dtypes.cs:38-50 block specs), -1 when the
+ * format is unsupported or n is not a whole number of blocks.
+ * qro_dequant_row: decodes n weights; returns 0, or -1 as above.           */
+long qro_row_bytes(int fmt, long n);
+int  qro_dequant_row(int fmt, const uint8_t* src, long n, float* dst);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,9 @@ PAGE_TOKENS = 256
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 DTYPES = {"f32": DTYPE_F32, "f16": DTYPE_F16, "bf16": DTYPE_BF16}
 
+# weight-row formats: QuantFormat values (Dtypes.cs:6-26)
+FORMATS = {"F32": 0, "F16": 1, "BF16": 2, "Q4_0": 3, "Q8_0": 4, "Q4_K": 6, "Q6_K": 7}
+
 QR_OK = 0
 QR_ERR_INVALID_ARGUMENT = -1
 QR_ERR_OUT_OF_RANGE = -2
@@ -100,6 +103,14 @@ SIGNATURES = {
     "qr_mla_bytes_used": [_p, _llp],
     "qr_mla_page_count": [_p, _i, _ip],
     "qr_mla_read_page": [_p, _i, _i, _p],
+    "qr_mla_attend_absorbed": [_p, _i, _i, _i, _i, _i, _p, _p, _p],
+    "qr_mla_attend_absorbed_dev": [_p, _i, _i, _i, _i, _i, _p, _p, _i, _p, _p],
+    "qr_weight_row_bytes": [_i, _i, _llp],
+    "qr_weight_create": [_pp, _i, ctypes.c_longlong, _i, _p],
+    "qr_weight_destroy": [_p],
+    "qr_weight_data": [_p, _pp],
+    "qr_mla_q_absorb_dev": [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
+    "qr_mla_wuv_dev": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
 }
 _RESTYPES = {"qr_last_error": ctypes.c_char_p, "qr_status_name": ctypes.c_char_p}
 

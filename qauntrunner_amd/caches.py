@@ -38,6 +38,11 @@ def _host_rows(x, src_dtype: int):
     return a
 
 
+def _dev_ptr(x):
+    """Device address of a torch tensor or of a weights.Weight."""
+    return ctypes.c_void_p(x.data_ptr())
+
+
 def _stream_ptr(stream):
     if stream is None:
         import torch
@@ -301,6 +306,25 @@ class MlaLatentCache:
         u = np.empty((heads, self.KvLora), np.float32)
         check(self._lib.qr_mla_attention(self._h, layer, pos, heads, _ptr(qt), _ptr(qr), scale, _ptr(u)))
         return u
+
+    def AttendAbsorbed(self, layer, pos, q, kvb, nope, vdim) -> np.ndarray:
+        """MlaLayer's absorbed block (StreamingEngine.cs:508-577) for one token: q [heads,
+        nope+rope] (rope part rotated), kvb a Weight of [heads*(nope+vdim), kv_lora].
+        Returns the attention output [heads, vdim]."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        heads = q.size // (nope + self.Rope)
+        out = np.empty((heads, vdim), np.float32)
+        check(self._lib.qr_mla_attend_absorbed(self._h, layer, pos, heads, nope, vdim, _ptr(q), kvb.handle,
+                                               _ptr(out)))
+        return out
+
+    def AttendAbsorbedDev(self, layer, pos, q, kvb, fmt, nope, vdim, out, stream=None) -> None:
+        """Device form: q, out torch tensors on the GPU; kvb a Weight or a uint8 device tensor
+        of rows in format `fmt`."""
+        heads = q.numel() // (nope + self.Rope)
+        check(self._lib.qr_mla_attend_absorbed_dev(self._h, layer, pos, heads, nope, vdim,
+                                                   ctypes.c_void_p(q.data_ptr()), _dev_ptr(kvb), fmt,
+                                                   ctypes.c_void_p(out.data_ptr()), _stream_ptr(stream)))
 
     def AbsorbedAttentionDev(self, layer, pos, q_tilde, q_rope, u, scale, stream=None) -> None:
         heads = q_tilde.numel() // self.KvLora

@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(256) rope_append_kernel(const RopeAppendArgs a
     __shared__ float cs[kRopeRows][2][kMaxRopeHalf];
     for (int idx = threadIdx.x; idx < kRopeRows * half; idx += 256) {
         const int r = idx / half, i = idx - r * half;
-        const float ang = __fmul_rn(static_cast<float>(g.pos0 + r0 + r), a.freq[i]);
+        const float ang = mul_rn(static_cast<float>(g.pos0 + r0 + r), a.freq[i]);
         cs[r][0][i] = cosf(ang);
         cs[r][1][i] = sinf(ang);
     }
@@ -146,8 +146,8 @@ __global__ void __launch_bounds__(256) rope_append_kernel(const RopeAppendArgs a
         float y0[4], y1[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            y0[e] = __fsub_rn(__fmul_rn(x0[e], cc[e]), __fmul_rn(x1[e], ss[e]));
-            y1[e] = __fadd_rn(__fmul_rn(x0[e], ss[e]), __fmul_rn(x1[e], cc[e]));
+            y0[e] = sub_rn(mul_rn(x0[e], cc[e]), mul_rn(x1[e], ss[e]));
+            y1[e] = add_rn(mul_rn(x0[e], ss[e]), mul_rn(x1[e], cc[e]));
         }
         if (h < kv_heads) {
             const int t = g.pos0 + r0 + r;

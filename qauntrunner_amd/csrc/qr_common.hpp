@@ -49,6 +49,24 @@ __host__ __device__ inline bool dtype_valid(int dt) {
     return dt == QR_DTYPE_F32 || dt == QR_DTYPE_F16 || dt == QR_DTYPE_BF16;
 }
 
+// ---------------------------------------------------------------- separately rounded ops
+// One IEEE fp32 multiply / add / subtract each, never fused into an FMA.  clang's HIP
+// __fmul_rn and friends are plain operators that inherit contraction from where they
+// are defined; these carry the pragma in their own bodies, so each product is rounded
+// before it is added, as the reference's RyuJIT code rounds it.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+
 // ---------------------------------------------------------------- device scalar codecs
 // 16-bit values travel as raw bits.  Decoding is exact.  Encoding follows the
 // reference codecs: Dtypes.FloatToF16 (Dtypes.cs:100-126) and

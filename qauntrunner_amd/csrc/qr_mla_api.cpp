@@ -1,9 +1,11 @@
 // qr_mla.cpp -- C ABI of the paged MLA latent cache (MlaLatentCache, MlaLatentCache.cs:10-65)
 // and of the absorbed attention over it (StreamingEngine.cs:531-568).
 #include <algorithm>
+#include <cmath>
 #include <new>
 
 #include "qr_mla.hpp"
+#include "qr_proj.hpp"
 #include "qr_store.hpp"
 
 using namespace qr;
@@ -16,6 +18,7 @@ struct qr_mla {
     hipStream_t stream = nullptr;
     DevBuf stage;
     DevBuf workspace;
+    DevBuf proj;  // q_tilde, u and q_rope of the absorbed layer call
 };
 
 namespace {
@@ -88,6 +91,34 @@ int attention_dev(qr_mla* m, int layer, int pos, int heads, const float* qt, con
     const MlaPlan plan = plan_mla(a);
     QR_TRY(m->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
     QR_HIP(launch_mla(a, plan, m->workspace.get(), stream));
+    return QR_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// StreamingEngine.cs:508-577 after cache.Append: q-absorb, absorbed attention, W_UV.
+int attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nope, int vdim, const float* q,
+                        const void* kvb, int fmt, float* out, hipStream_t stream) {
+    MlaProjArgs a{};
+    QR_TRY(mla_proj_prepare(a, kvb, fmt, heads, nope, m->rope, vdim, m->kv_lora));
+    const size_t qt_bytes = align256(static_cast<size_t>(heads) * m->kv_lora * 4);
+    const size_t qr_bytes = align256(static_cast<size_t>(heads) * std::max(m->rope, 1) * 4);
+    QR_TRY(m->proj.ensure(2 * qt_bytes + qr_bytes));
+    char* base = static_cast<char*>(m->proj.get());
+    float* qt = reinterpret_cast<float*>(base);
+    float* u = reinterpret_cast<float*>(base + qt_bytes);
+    float* qr_ = reinterpret_cast<float*>(base + 2 * qt_bytes);
+    a.nq = 1;
+    a.in = q;
+    a.out = qt;
+    a.q_rope = m->rope > 0 ? qr_ : nullptr;
+    QR_HIP(launch_mla_absorb(a, stream));
+    const float scale = 1.0f / std::sqrt(static_cast<float>(nope + m->rope));  // :511
+    QR_TRY(attention_dev(m, layer, pos, heads, qt, qr_, scale, u, stream));
+    a.in = u;
+    a.out = out;
+    a.q_rope = nullptr;
+    QR_HIP(launch_mla_wuv(a, stream));
     return QR_OK;
 }
 
@@ -243,6 +274,42 @@ int qr_mla_attention_dev(qr_mla* m, int layer, int pos, int heads, const float* 
     DeviceGuard dg(m->device);
     return attention_dev(m, layer, pos, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
                          static_cast<hipStream_t>(stream));
+}
+
+int qr_mla_attend_absorbed(qr_mla* m, int layer, int pos, int heads, int nope, int vdim, const float* q,
+                           const qr_weight* kvb, float* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(q && out && kvb, "null q / kvb / out pointer");
+    QR_TRY(validate_attention(m, layer, pos, heads));
+    QR_CHECK_ARG(nope >= 1 && vdim >= 1, "bad nope %d / vdim %d", nope, vdim);
+    QR_CHECK_ARG(kvb->rows == static_cast<long long>(heads) * (nope + vdim) && kvb->cols == m->kv_lora,
+                 "kvb is %lld x %d, expected %lld x %d", kvb->rows, kvb->cols,
+                 static_cast<long long>(heads) * (nope + vdim), m->kv_lora);
+    QR_CHECK_ARG(kvb->device == m->device, "kvb lives on device %d, the cache on %d", kvb->device, m->device);
+    DeviceGuard dg(m->device);
+    const size_t q_bytes = static_cast<size_t>(heads) * (nope + m->rope) * 4;
+    const size_t o_bytes = static_cast<size_t>(heads) * vdim * 4;
+    QR_TRY(m->stage.ensure(align256(q_bytes) + o_bytes));
+    char* st = static_cast<char*>(m->stage.get());
+    float* dq = reinterpret_cast<float*>(st);
+    float* dout = reinterpret_cast<float*>(st + align256(q_bytes));
+    QR_HIP(hipMemcpyAsync(dq, q, q_bytes, hipMemcpyHostToDevice, m->stream));
+    QR_TRY(attend_absorbed_dev(m, layer, pos, heads, nope, vdim, dq, kvb->dev, kvb->format, dout, m->stream));
+    QR_HIP(hipMemcpyAsync(out, dout, o_bytes, hipMemcpyDeviceToHost, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+int qr_mla_attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nope, int vdim, const float* q_dev,
+                               const void* kvb_dev, int kvb_format, float* out_dev, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(q_dev && out_dev, "null q / out pointer");
+    QR_TRY(validate_attention(m, layer, pos, heads));
+    DeviceGuard dg(m->device);
+    return attend_absorbed_dev(m, layer, pos, heads, nope, vdim, q_dev, kvb_dev, kvb_format, out_dev,
+                               static_cast<hipStream_t>(stream));
 }
 
 int qr_mla_reset(qr_mla* m) {

@@ -1,0 +1,95 @@
+"""HBM-resident weight tensors and the MLA projections over them.
+
+``Weight`` is one tensor of a ModelStore (ModelStore.cs: a format, a row count,
+``RowBytes`` per row) uploaded once to the GPU; the projections decode its rows
+on the fly exactly as BlockDequantizer.Dequantize (Core/Quantization/
+BlockDequantizer.cs) and follow the reference's fp32 operation order, so their
+results equal the reference's bit for bit.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import FORMATS, check
+
+__all__ = ["Weight", "row_bytes", "format_code", "mla_q_absorb_dev", "mla_wuv_dev"]
+
+
+def format_code(fmt) -> int:
+    return fmt if isinstance(fmt, int) else FORMATS[fmt]
+
+
+def row_bytes(fmt, cols: int) -> int:
+    """Bytes of one row of `cols` weights (Dtypes.TensorBytes)."""
+    out = ctypes.c_longlong()
+    check(_lib.load().qr_weight_row_bytes(format_code(fmt), cols, ctypes.byref(out)))
+    return out.value
+
+
+class Weight:
+    """A [rows, cols] weight tensor in one QuantFormat, uploaded from its raw bytes."""
+
+    def __init__(self, fmt, rows: int, cols: int, raw: np.ndarray):
+        self._lib = _lib.load()
+        self.Fmt = format_code(fmt)
+        self.Rows, self.Cols = rows, cols
+        self.RowBytes = row_bytes(self.Fmt, cols)
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        if raw.size != rows * self.RowBytes:
+            raise ValueError(f"expected {rows * self.RowBytes} bytes, got {raw.size}")
+        h = ctypes.c_void_p()
+        check(self._lib.qr_weight_create(ctypes.byref(h), self.Fmt, rows, cols,
+                                          raw.ctypes.data_as(ctypes.c_void_p)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def data_ptr(self) -> int:
+        p = ctypes.c_void_p()
+        check(self._lib.qr_weight_data(self._h, ctypes.byref(p)))
+        return p.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.qr_weight_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _dev(x):
+    """Device address of a Weight or of a torch tensor."""
+    return ctypes.c_void_p(x.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(getattr(stream, "cuda_stream", stream))
+
+
+def mla_q_absorb_dev(kvb, fmt, heads, nope, rope, vdim, kv_lora, q, q_tilde, stream=None) -> None:
+    """q_tilde[b,h,:] = sum_j q[b,h,j] * W_kvb[h*(nope+vdim)+j, :] (StreamingEngine.cs:517-529)."""
+    nq = q.numel() // (heads * (nope + rope))
+    check(_lib.load().qr_mla_q_absorb_dev(_dev(kvb), format_code(fmt), heads, nope, rope, vdim, kv_lora, nq,
+                                          ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(q_tilde.data_ptr()),
+                                          _stream(stream)))
+
+
+def mla_wuv_dev(kvb, fmt, heads, nope, vdim, kv_lora, u, out, stream=None) -> None:
+    """out[b,h,j] = DotF32(W_kvb[h*(nope+vdim)+nope+j, :], u[b,h]) (StreamingEngine.cs:569-576)."""
+    nq = u.numel() // (heads * kv_lora)
+    check(_lib.load().qr_mla_wuv_dev(_dev(kvb), format_code(fmt), heads, nope, vdim, kv_lora, nq,
+                                     ctypes.c_void_p(u.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                     _stream(stream)))

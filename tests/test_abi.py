@@ -71,3 +71,30 @@ def test_status_maps_to_python_exceptions():
     with pytest.raises(qr.QrInvalidArgument):
         qr.PagedKvCache(1, 8, 2, 48, 512)
     assert issubclass(qr.QrOutOfRange, IndexError) and issubclass(qr.QrNotResident, LookupError)
+
+
+def test_weight_row_bytes_match_the_oracle():
+    """Dtypes.cs:38-50 block specs through the C ABI, for every decoded format."""
+    from oracle import oracle
+    from qauntrunner_amd import weights
+
+    for name, code in _lib.FORMATS.items():
+        for cols in (256, 512, 1024):
+            assert weights.row_bytes(code, cols) == oracle.row_bytes(code, cols), (name, cols)
+    for fmt, cols in ((5, 256), (3, 48), (6, 128), (99, 8)):
+        with pytest.raises(qr.QrInvalidArgument):
+            weights.row_bytes(fmt, cols)
+
+
+def test_projection_arguments_validate_before_device():
+    L = qr.load()
+    null = ctypes.c_void_p()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+    assert L.qr_mla_q_absorb_dev(null, 2, 8, 128, 64, 128, 512, 1, fake, fake, null) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_q_absorb_dev(fake, 5, 8, 128, 64, 128, 512, 1, fake, fake, null) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_wuv_dev(fake, 2, 8, 128, 128, 500, 1, fake, fake, null) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_wuv_dev(ctypes.c_void_p(0x1002), 2, 8, 128, 128, 512, 1, fake, fake, null) == \
+        _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_attend_absorbed(null, 0, 0, 8, 128, 128, fake, fake, fake) == _lib.QR_ERR_INVALID_ARGUMENT
+    h = ctypes.c_void_p()
+    assert L.qr_weight_create(ctypes.byref(h), 4, 4, 48, fake) == _lib.QR_ERR_INVALID_ARGUMENT and not h.value

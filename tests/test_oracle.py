@@ -288,3 +288,94 @@ def test_reference_growth_bug_is_where_documented():
     assert first == 768 and nulls == [3]
     first, nulls = paging.reference_growth_null_pages(700)
     assert first is None and nulls == [3]
+
+
+# ------------------------------------------------------------------ weight-row decoders
+from tests import quant  # noqa: E402
+
+
+def test_q4_0_known_answer_from_reference_test():
+    """Tests/Program.cs:449-457 (hand-built Q4_0: d = f16(-0.5), bytes 0x08 and 0x2A).  The
+    reference's block has 2 more pad bytes (BlockDequantizer.cs:52-69); the nibble order is
+    the same: low nibble of byte i is weight i, high nibble weight i+16."""
+    blk = np.zeros(20, np.uint8)
+    blk[0], blk[1], blk[2], blk[3] = 0x00, 0xB8, 0x08, 0x2A
+    y = oracle.dequant_rows(quant.FMT["Q4_0"], blk, 32)[0]
+    assert (y[0], y[16], y[1], y[17]) == (0.0, 4.0, -1.0, 3.0)
+    assert np.all(y[2:16] == 4.0) and np.all(y[18:] == 4.0)  # zero bytes -> (0-8)*(-0.5)
+
+
+def test_q8_0_and_fp_rows_closed_form():
+    rng = np.random.default_rng(3)
+    q = rng.integers(-128, 128, 64).astype(np.int8)
+    raw = np.zeros((1, 68), np.uint8)
+    for b, d in enumerate((0.25, -3.0)):
+        raw[0, 34 * b:34 * b + 2] = np.float16(d).reshape(1).view(np.uint8)
+        raw[0, 34 * b + 2:34 * b + 34] = q[32 * b:32 * b + 32].view(np.uint8)
+    y = oracle.dequant_rows(quant.FMT["Q8_0"], raw, 64)[0]
+    assert np.array_equal(y, np.concatenate([0.25 * q[:32], -3.0 * q[32:]]).astype(F32))
+    x = normal(4, (3, 40))
+    for name in ("F32", "F16", "BF16"):
+        f = quant.FMT[name]
+        got = oracle.dequant_rows(f, quant.quantize(f, x), 40)
+        want = {"F32": x, "F16": x.astype(np.float16).astype(F32),
+                "BF16": oracle.bf16_to_f32(oracle.f32_to_bf16(x))}[name]
+        assert np.array_equal(got, want), name
+
+
+def test_q4_k_layout_closed_form():
+    """Every sub-block gets its own 6-bit scale and min (values >= 16 exercise the high-bit
+    packing of sub-blocks 4..7) and every nibble a known value; d and dmin are powers of two
+    so d*sc*q - dmin*m is exact and the layout alone decides the result."""
+    rng = np.random.default_rng(5)
+    sc = np.array([1, 7, 16, 63, 33, 17, 48, 5])
+    mn = np.array([0, 63, 9, 20, 47, 31, 16, 62])
+    q = rng.integers(0, 16, 256)
+    d, dmin = 2.0 ** -6, 2.0 ** -9
+    blk = quant.build_q4k_block(d, dmin, sc, mn, q)
+    assert np.array_equal(blk, quant.pack_q4k(np.array([d]), np.array([dmin]), sc[None], mn[None], q[None])[0])
+    y = oracle.dequant_rows(quant.FMT["Q4_K"], blk, 256)[0].astype(np.float64)
+    sub = np.arange(256) // 32
+    assert np.array_equal(y, d * sc[sub] * q - dmin * mn[sub])
+
+
+def test_q6_k_layout_closed_form():
+    """Each 6-bit value has one low-nibble and one 2-bit slot (the slots tile the 192 bytes
+    exactly once) and each group of 16 its own int8 scale."""
+    slots = set()
+    for w in range(256):
+        ql, hi, qh, sh, _ = quant.q6k_slots(w)
+        slots.add(("l", ql, hi))
+        slots.add(("h", qh, sh))
+    assert len(slots) == 512 and {s[1] for s in slots if s[0] == "l"} == set(range(128))
+    rng = np.random.default_rng(6)
+    q = rng.integers(0, 64, 256)
+    sc = np.array([1, -2, 3, -4, 127, -128, 7, 8, 9, -10, 11, 12, -13, 14, 15, 100])
+    d = 2.0 ** -10
+    blk = quant.build_q6k_block(d, sc, q)
+    assert np.array_equal(blk, quant.pack_q6k(np.array([d]), sc[None], q[None])[0])
+    y = oracle.dequant_rows(quant.FMT["Q6_K"], blk, 256)[0].astype(np.float64)
+    k = np.array([quant.q6k_scale_index(w) for w in range(256)])
+    assert np.array_equal(y, d * sc[k] * (q - 32))
+
+
+@pytest.mark.parametrize("name,tol", [("Q8_0", 0.02), ("Q6_K", 0.03), ("Q4_0", 0.11), ("Q4_K", 0.09)])
+def test_quant_round_trip_rms(name, tol):
+    """Tests/Program.cs:96-127 (QuantRoundTrip): N(0, 0.5^2) weights, 32 blocks, relative RMS
+    within the reference's per-format bound."""
+    f = quant.FMT[name]
+    bs = quant.BLOCK[f][0]
+    x = (np.random.default_rng(7).standard_normal((1, bs * 32)) * 0.5).astype(F32)
+    raw = quant.quantize(f, x)
+    assert raw.shape[1] == oracle.row_bytes(f, bs * 32)
+    y = oracle.dequant_rows(f, raw, bs * 32)
+    rms = math.sqrt(np.mean((y - x) ** 2)) / math.sqrt(np.mean(x ** 2))
+    assert rms <= tol, f"{name}: rel RMS {rms:.3f}"
+
+
+def test_row_bytes_and_unsupported_formats():
+    assert oracle.row_bytes(quant.FMT["Q4_K"], 512) == 288 and oracle.row_bytes(quant.FMT["Q6_K"], 256) == 210
+    assert oracle.row_bytes(quant.FMT["Q4_0"], 64) == 40 and oracle.row_bytes(quant.FMT["F32"], 3) == 12
+    for fmt, n in ((5, 256), (8, 64), (quant.FMT["Q8_0"], 48), (quant.FMT["Q4_K"], 128)):
+        with pytest.raises(ValueError):
+            oracle.row_bytes(fmt, n)
