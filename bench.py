@@ -67,7 +67,25 @@ WORKLOADS = {
     "f2-mla-layer-q8": dict(kind="mla_layer", heads=128, kv_lora=512, rope_dim=64, nope=128, vdim=128, n=16384,
                             dtype="bf16", kvb_fmt="Q8_0", B=1,
                             desc="MLA absorbed layer block as f2-mla-layer with the kvb weights in Q8_0"),
+    "f3-matvec-q4k": dict(kind="matvec", wfmt="Q4_K", dtype="f32", B=1,
+                          desc="fused dequant + dot MatVecs of one llama-3-8b layer for one token: wq, wk, wv, wo "
+                               "(4096/1024 x 4096), gate, up (14336 x 4096), down (4096 x 14336), Q4_K weights"),
+    "f3-matvec-q8": dict(kind="matvec", wfmt="Q8_0", dtype="f32", B=1,
+                         desc="the f3-matvec-q4k projections with Q8_0 weights"),
+    "f3-matvec-f16": dict(kind="matvec", wfmt="F16", dtype="f32", B=1,
+                          desc="the f3-matvec-q4k projections with F16 weights"),
 }
+
+# llama-3-8b layer projections (rows, cols): wq, wk, wv, wo, gate, up, down
+MATVEC_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
+                 (4096, 14336)]
+W_FORMATS = {"F16": (1, 1, 2), "Q8_0": (4, 32, 34), "Q4_K": (6, 256, 144)}  # code, block, bytes
+
+
+def matvec_bytes(w):
+    code, bs, bb = W_FORMATS[w["wfmt"]]
+    return sum(r * (c // bs) * bb + c * 4 + r * 4 for r, c in MATVEC_SHAPES)
+
 
 KVB_FORMATS = {"F32": (0, 1, 4), "F16": (1, 1, 2), "BF16": (2, 1, 2), "Q8_0": (4, 32, 34)}  # code, block, bytes
 
@@ -103,6 +121,9 @@ def algorithmic(w):
         b = w["n"] * width * esize(w["dtype"]) + w["heads"] * width * 4 + w["heads"] * w["kv_lora"] * 4 + pages * 4
         f = 2 * w["heads"] * w["n"] * (width + w["kv_lora"])
         return b, f
+    if w["kind"] == "matvec":
+        # every weight byte once + x in + y out per matrix; 2 flops per weight
+        return matvec_bytes(w), sum(2 * r * c for r, c in MATVEC_SHAPES)
     if w["kind"] == "mla_layer":
         # latents + every kvb row once + q in + out; the q~/u hand-offs between kernels are not counted
         width = w["kv_lora"] + w["rope_dim"]
@@ -236,6 +257,23 @@ def run_gpu(w, steps, warmup):
                 "wuv": lambda r: qr.mla_wuv_dev(kvbs[r], code, H, nope, vdim, L, qt_scratch[r], out[r],
                                                 stream=stream)}
         qt_scratch = torch.randn(R, H, L, device=dev, generator=gen)
+    elif w["kind"] == "matvec":
+        code, bs, bb = W_FORMATS[w["wfmt"]]
+        set_bytes = matvec_bytes(w)
+        R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
+        mats = [[synth_weights(w["wfmt"], r, c, gen, dev) for r, c in MATVEC_SHAPES] for _ in range(R)]
+        xs = [torch.randn(c, device=dev, generator=gen) for _, c in MATVEC_SHAPES]
+        ys = [torch.empty(r, device=dev) for r, _ in MATVEC_SHAPES]
+
+        def step(i):
+            m = mats[i % R]
+            for k, (r, c) in enumerate(MATVEC_SHAPES):
+                qr.matvec_dev(m[k], code, r, c, xs[k], ys[k], stream=stream)
+
+        class _NoHandle:
+            def close(self):
+                pass
+        handle = _NoHandle()
     elif w["kind"] == "rope":
         n, kvd, qd = w["n"], w["kv"] * w["D"], w["heads"] * w["D"]
         set_bytes = n * (qd + 2 * kvd) * 4
@@ -304,6 +342,25 @@ def run_gpu(w, steps, warmup):
             extra[name] = t0.elapsed_time(t1) / steps
     handle.close()
     return ms, wall * 1e3 / steps, kernel_ms, extra
+
+
+def synth_weights(fmt, rows, cols, gen, dev):
+    """rows x cols weights in fmt as a uint8 device tensor: N(0, 0.05^2) for F16; for the block
+    formats random quant bytes under small fixed f16 scales (every byte pattern is a valid
+    block once the scale fields are finite)."""
+    import torch
+
+    if fmt == "F16":
+        return (torch.randn(rows, cols, device=dev, generator=gen) * 0.05).half().view(torch.uint8).reshape(-1)
+    code, bs, bb = W_FORMATS[fmt]
+    blocks = rows * cols // bs
+    raw = torch.randint(0, 256, (blocks, bb), dtype=torch.uint8, device=dev, generator=gen)
+    if fmt == "Q8_0":
+        raw[:, 0:2] = torch.full((blocks,), 0.05 / 127, dtype=torch.float16, device=dev).view(torch.uint8).view(blocks, 2)
+    else:  # Q4_K: d, dmin
+        raw[:, 0:2] = torch.full((blocks,), 0.05 / 15 / 32, dtype=torch.float16, device=dev).view(torch.uint8).view(blocks, 2)
+        raw[:, 2:4] = torch.full((blocks,), 0.05 / 63, dtype=torch.float16, device=dev).view(torch.uint8).view(blocks, 2)
+    return raw.reshape(-1)
 
 
 def synth_kvb(w, gen, dev):
@@ -391,6 +448,30 @@ def cpu_baseline(w, budget_s=10.0):
             return qr_
         unit_fraction = sample_rows / w["n"]
         sample = f"{sample_rows} of {w['n']} positions, fp32 storage"
+    elif w["kind"] == "matvec":
+        code, bs, bb = W_FORMATS[w["wfmt"]]
+        sample_rows = 32
+        mats = []
+        for r, c in MATVEC_SHAPES:
+            if w["wfmt"] == "F16":
+                raw = (rng.standard_normal((sample_rows, c)) * 0.05).astype(np.float16).view(np.uint8)
+            else:  # random quant bytes under the same fixed scales as the device synthesis
+                raw = rng.integers(0, 256, (sample_rows * c // bs, bb), dtype=np.uint8)
+                if w["wfmt"] == "Q8_0":
+                    raw[:, 0:2] = np.float16(0.05 / 127).reshape(1).view(np.uint8)
+                else:
+                    raw[:, 0:2] = np.float16(0.05 / 15 / 32).reshape(1).view(np.uint8)
+                    raw[:, 2:4] = np.float16(0.05 / 63).reshape(1).view(np.uint8)
+            mats.append((np.ascontiguousarray(raw).reshape(sample_rows, -1), c,
+                         rng.standard_normal(c).astype(np.float32)))
+        total_rows = sum(r for r, _ in MATVEC_SHAPES)
+
+        def call():  # DotRow over a sample of every matrix's rows
+            for raw, c, x in mats:
+                oracle.matvec(code, raw, c, x)
+        unit_fraction = len(MATVEC_SHAPES) * sample_rows / total_rows
+        sample = (f"DotRow over {sample_rows} rows of each of the 7 matrices ({len(MATVEC_SHAPES) * sample_rows} of "
+                  f"{total_rows} rows), scaled to all rows")
     elif w["kind"] == "mla_layer":
         width = w["kv_lora"] + w["rope_dim"]
         H, nope, vdim, L, rp = w["heads"], w["nope"], w["vdim"], w["kv_lora"], w["rope_dim"]

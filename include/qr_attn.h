@@ -241,6 +241,15 @@ int qr_mla_q_absorb_dev(const void* kvb_dev, int kvb_format, int heads, int nope
  * out_dev [nq][heads][vdim]. */
 int qr_mla_wuv_dev(const void* kvb_dev, int kvb_format, int heads, int nope, int vdim, int kv_lora,
                    int nq, const float* u_dev, float* out_dev, void* stream);
+/* MatVec / MatVecParallel, DotKernels.cs:599-633: y[b][r] = DotRow(W row r, x[b]) for nq input
+ * vectors, each row in its format's own fused dequant + dot order (DotKernels.cs:24-447), so
+ * every y[r] equals the reference's bit for bit.  w_dev [rows][row bytes] 16-byte aligned;
+ * x_dev [nq][cols] 16-byte aligned; y_dev [nq][rows].  cols: whole blocks of the format,
+ * and a multiple of 8 for F32/F16/BF16. */
+int qr_matvec_dev(const void* w_dev, int format, long long rows, int cols, int nq, const float* x_dev,
+                  float* y_dev, void* stream);
+/* Same with host vectors against an uploaded weight (synchronous; not thread-safe per weight). */
+int qr_matvec(const qr_weight* w, int nq, const float* x, float* y);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,8 @@ def lib():
             "qro_mla_expanded_f64": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i, _i, _i, _d, _f64p]),
             "qro_row_bytes": (ctypes.c_long, [_i, _l]),
             "qro_dequant_row": (ctypes.c_int, [_i, _u8p, _l, _f32p]),
+            "qro_dot_row": (ctypes.c_float, [_i, _u8p, _f32p, _i]),
+            "qro_matvec": (ctypes.c_int, [_i, _u8p, _l, _i, _f32p, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -222,3 +224,14 @@ def dequant_rows(fmt, raw, n):
         if lib().qro_dequant_row(int(fmt), raw[r], n, out[r]) != 0:
             raise ValueError(f"format {fmt} unsupported")
     return out
+
+
+def matvec(fmt, raw, cols, x):
+    """DotKernels.MatVec: y[r] = DotRow(fmt, row r of raw, x) in the reference's per-format order."""
+    rb = row_bytes(fmt, cols)
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, rb)
+    x = _c32(x).reshape(-1)
+    y = np.empty(raw.shape[0], np.float32)
+    if lib().qro_matvec(int(fmt), raw.reshape(-1), raw.shape[0], cols, x, y) != 0:
+        raise ValueError(f"format {fmt} unsupported")
+    return y

@@ -495,3 +495,207 @@ int qro_dequant_row(int fmt, const uint8_t* s, long n, float* y)
     }
     return -1;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Fused dequant + dot rows: Core/Kernels/DotKernels.cs                       */
+/* ------------------------------------------------------------------------- */
+
+/* SimdMath.cs:17-22: lane sum in lane order. */
+static float hsum8(const float* v)
+{
+    float s = 0.0f;
+    for (int i = 0; i < 8; i++) s += v[i];
+    return s;
+}
+
+/* DotKernels.cs:86-100 (HalfBitsToFloat): normals by exponent re-bias, subnormals as
+ * mantissa * 2^-24; exponent 31 is NOT special-cased, so f16 inf/NaN come out as finite
+ * values 2^16 * (1 + m/1024). */
+static float f16_vec_decode(uint16_t h)
+{
+    uint32_t u = h;
+    uint32_t sign = (u & 0x8000u) << 16, exp = (u >> 10) & 0x1Fu, man = (u & 0x3FFu) << 13;
+    if (exp == 0) {
+        float sub = (float)(u & 0x3FFu) * 5.9604645e-8f;
+        return u2f(f2u(sub) | sign);
+    }
+    return u2f(sign | ((exp + 112u) << 23) | man);
+}
+
+/* DotKernels.cs:59-84 (F16), :106-128 (BF16), SimdMath.cs:34-53 (F32): 8 lane sums over
+ * k = 8c + L, HSum, then a sequential tail (tail halves decoded by Dtypes.F16ToFloat). */
+static float dot_fp(int fmt, const uint8_t* w, const float* x, int cols)
+{
+    const uint16_t* s = (const uint16_t*)w;
+    if (fmt == 0) return qro_dot_f32((const float*)w, x, cols);
+    if (cols >= 8) {
+        float lanes[8] = {0};
+        int i = 0;
+        for (; i + 8 <= cols; i += 8)
+            for (int j = 0; j < 8; j++) {
+                float wv = fmt == 1 ? f16_vec_decode(s[i + j]) : qro_bf16_to_f32(s[i + j]);
+                float p = wv * x[i + j];
+                lanes[j] = lanes[j] + p;
+            }
+        float sum = hsum8(lanes);
+        for (; i < cols; i++) {
+            float wv = fmt == 1 ? qro_f16_to_f32(s[i]) : qro_bf16_to_f32(s[i]);
+            float p = wv * x[i];
+            sum = sum + p;
+        }
+        return sum;
+    }
+    float ss = 0.0f;
+    for (int i = 0; i < cols; i++) {
+        float wv = fmt == 1 ? qro_f16_to_f32(s[i]) : qro_bf16_to_f32(s[i]);
+        float p = wv * x[i];
+        ss = ss + p;
+    }
+    return ss;
+}
+
+/* DotKernels.cs:134-178: per block, lane L of accQ takes lo[L]x[L], lo[8+L]x[8+L],
+ * hi[L]x[16+L], hi[8+L]x[24+L]; accX the same x's; sum += d*dotQ - 8*d*sumX. */
+static float dot_q4_0(const uint8_t* w, const float* x, int cols)
+{
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++, w += 20, x += 32) {
+        float d = qro_f16_to_f32(le16(w));
+        float aq[8], ax[8];
+        for (int L = 0; L < 8; L++) {
+            float q0 = (float)(w[2 + L] & 0xF), q1 = (float)(w[2 + 8 + L] & 0xF);
+            float q2 = (float)(w[2 + L] >> 4), q3 = (float)(w[2 + 8 + L] >> 4);
+            float a = 0.0f, s = 0.0f, p;
+            p = q0 * x[L]; a = a + p;
+            p = q1 * x[8 + L]; a = a + p;
+            p = q2 * x[16 + L]; a = a + p;
+            p = q3 * x[24 + L]; a = a + p;
+            s = s + x[L]; s = s + x[8 + L]; s = s + x[16 + L]; s = s + x[24 + L];
+            aq[L] = a;
+            ax[L] = s;
+        }
+        float dotq = hsum8(aq), sumx = hsum8(ax);
+        float t1 = d * dotq, d8 = 8.0f * d, t2 = d8 * sumx, e = t1 - t2;
+        sum = sum + e;
+    }
+    return sum;
+}
+
+/* DotKernels.cs:183-230 (DotQ8_0, DotI8Bytes): lane L takes q[L], q[8+L], q[16+L], q[24+L];
+ * HSum; sum += d * dot. */
+static float dot_q8_0(const uint8_t* w, const float* x, int cols)
+{
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 32; b++, w += 34, x += 32) {
+        float d = qro_f16_to_f32(le16(w));
+        float acc[8];
+        for (int L = 0; L < 8; L++) {
+            float a = 0.0f;
+            for (int k = 0; k < 4; k++) {
+                float p = (float)(int8_t)w[2 + 8 * k + L] * x[8 * k + L];
+                a = a + p;
+            }
+            acc[L] = a;
+        }
+        float dot = hsum8(acc), e = d * dot;
+        sum = sum + e;
+    }
+    return sum;
+}
+
+/* DotKernels.cs:361-373 (VecDot16): lane L = q[L]x[L] + q[8+L]x[8+L] (no leading zero), HSum. */
+static float vecdot16(const float* q, const float* x)
+{
+    float acc[8];
+    for (int L = 0; L < 8; L++) {
+        float p0 = q[L] * x[L], p1 = q[8 + L] * x[8 + L];
+        acc[L] = p0 + p1;
+    }
+    return hsum8(acc);
+}
+
+/* DotKernels.cs:264-270 (SubSum): sequential. */
+static float subsum(const float* x, int n)
+{
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s = s + x[i];
+    return s;
+}
+
+/* DotKernels.cs:322-358: per 64-weight group j, even sub-block (low nibbles of the 32
+ * bytes) then odd (high nibbles): sum += a*(VecDot16 + VecDot16) - mm*SubSum(32). */
+static float dot_q4_k(const uint8_t* w, const float* x, int cols)
+{
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 256; b++, w += 144, x += 256) {
+        float d = qro_f16_to_f32(le16(w)), dmin = qro_f16_to_f32(le16(w + 2));
+        const uint8_t* q = w + 16;
+        for (int j = 0; j < 4; j++, q += 32) {
+            for (int odd = 0; odd < 2; odd++) {
+                int sc, m;
+                scale_min_k4(2 * j + odd, w + 4, &sc, &m);
+                float a = d * (float)sc, mm = dmin * (float)m;
+                float lo[16], hi[16];
+                for (int i = 0; i < 16; i++) {
+                    lo[i] = (float)(odd ? (q[i] >> 4) : (q[i] & 0xF));
+                    hi[i] = (float)(odd ? (q[16 + i] >> 4) : (q[16 + i] & 0xF));
+                }
+                const float* xs = x + j * 64 + 32 * odd;
+                float v1 = vecdot16(lo, xs), v2 = vecdot16(hi, xs + 16), v = v1 + v2;
+                float t1 = a * v, t2 = mm * subsum(xs, 32), e = t1 - t2;
+                sum = sum + e;
+            }
+        }
+    }
+    return sum;
+}
+
+/* DotKernels.cs:420-447: dot += (float)(sc*(q-32)) * x in (half, l, q1..q4) order; sum += d*dot. */
+static float dot_q6_k(const uint8_t* w, const float* x, int cols)
+{
+    float sum = 0.0f;
+    for (int b = 0; b < cols / 256; b++, w += 210, x += 256) {
+        float d = qro_f16_to_f32(le16(w + 208));
+        const uint8_t *ql = w, *qh = w + 128;
+        const int8_t* sc = (const int8_t*)(w + 192);
+        float dot = 0.0f;
+        for (int n = 0; n < 256; n += 128) {
+            int sb = 8 * (n / 128);
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16;
+                int q1 = (ql[n / 2 + l] & 0xF) | (((qh[n / 4 + l] >> 0) & 3) << 4);
+                int q2 = (ql[n / 2 + l + 32] & 0xF) | (((qh[n / 4 + l] >> 2) & 3) << 4);
+                int q3 = (ql[n / 2 + l] >> 4) | (((qh[n / 4 + l] >> 4) & 3) << 4);
+                int q4 = (ql[n / 2 + l + 32] >> 4) | (((qh[n / 4 + l] >> 6) & 3) << 4);
+                float p;
+                p = (float)(sc[sb + is + 0] * (q1 - 32)) * x[n + l]; dot = dot + p;
+                p = (float)(sc[sb + is + 2] * (q2 - 32)) * x[n + l + 32]; dot = dot + p;
+                p = (float)(sc[sb + is + 4] * (q3 - 32)) * x[n + l + 64]; dot = dot + p;
+                p = (float)(sc[sb + is + 6] * (q4 - 32)) * x[n + l + 96]; dot = dot + p;
+            }
+        }
+        float e = d * dot;
+        sum = sum + e;
+    }
+    return sum;
+}
+
+float qro_dot_row(int fmt, const uint8_t* w, const float* x, int cols)
+{
+    switch (fmt) {
+    case 0: case 1: case 2: return dot_fp(fmt, w, x, cols);
+    case 3: return dot_q4_0(w, x, cols);
+    case 4: return dot_q8_0(w, x, cols);
+    case 6: return dot_q4_k(w, x, cols);
+    case 7: return dot_q6_k(w, x, cols);
+    }
+    return NAN;
+}
+
+int qro_matvec(int fmt, const uint8_t* w, long rows, int cols, const float* x, float* y)
+{
+    long rb = qro_row_bytes(fmt, cols);
+    if (rb < 0) return -1;
+    for (long r = 0; r < rows; r++) y[r] = qro_dot_row(fmt, w + r * rb, x, cols);
+    return 0;
+}

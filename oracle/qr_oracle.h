@@ -82,6 +82,13 @@ void qro_mla_expanded_f64(const float* q, const float* kvb, const float* lat, in
 long qro_row_bytes(int fmt, long n);
 int  qro_dequant_row(int fmt, const uint8_t* src, long n, float* dst);
 
+/* ---- fused dequant + dot: Core/Kernels/DotKernels.cs ----
+ * qro_dot_row: DotRow (:24-46) for the formats above, in each format's own operation
+ * order (:52-447).  qro_matvec: MatVec (:599-608), y[r] = DotRow(row r, x); -1 when the
+ * format cannot hold rows of `cols` weights.                                      */
+float qro_dot_row(int fmt, const uint8_t* w, const float* x, int cols);
+int   qro_matvec(int fmt, const uint8_t* w, long rows, int cols, const float* x, float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,11 +19,11 @@ from ._lib import (
     load,
 )
 from .caches import MlaLatentCache, PagedKvCache, dtype_code
-from .weights import Weight, mla_q_absorb_dev, mla_wuv_dev
+from .weights import Weight, matvec_dev, mla_q_absorb_dev, mla_wuv_dev
 
 __all__ = [
     "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "LIB_PATH", "PAGE_TOKENS",
     "QrError", "QrHipError", "QrInvalidArgument", "QrNotResident", "QrOutOfMemory", "QrOutOfRange",
     "load", "MlaLatentCache", "PagedKvCache", "dtype_code",
-    "Weight", "mla_q_absorb_dev", "mla_wuv_dev",
+    "Weight", "matvec_dev", "mla_q_absorb_dev", "mla_wuv_dev",
 ]

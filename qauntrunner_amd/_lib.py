@@ -111,6 +111,8 @@ SIGNATURES = {
     "qr_weight_data": [_p, _pp],
     "qr_mla_q_absorb_dev": [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     "qr_mla_wuv_dev": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
+    "qr_matvec_dev": [_p, _i, ctypes.c_longlong, _i, _i, _p, _p, _p],
+    "qr_matvec": [_p, _i, _p, _p],
 }
 _RESTYPES = {"qr_last_error": ctypes.c_char_p, "qr_status_name": ctypes.c_char_p}
 

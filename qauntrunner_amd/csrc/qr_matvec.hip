@@ -1,0 +1,654 @@
+// qr_matvec.hip -- fused dequant + dot MatVec y = W x over block-quantized rows
+// (DotKernels.MatVec / MatVecParallel, DotKernels.cs:599-633), in each format's own
+// fp32 operation order (DotRow, DotKernels.cs:24-447) so that every y[r] equals the
+// reference's bit for bit:
+//   F32/BF16/F16  8 lane sums over k = 8c + L, then 0 + lane0 + ... + lane7
+//                 (F16 decodes exponent 31 as a finite 2^16-scale value, as the
+//                 reference's vector converter HalfBitsToFloat does, :86-100)
+//   Q8_0          per block: lanes over q[L], q[8+L], q[16+L], q[24+L]; HSum; sum += d*dot
+//   Q4_0          per block: lanes over lo/hi nibbles; sum += d*dotQ - 8*d*sumX
+//   Q4_K          per sub-block: sum += a*(VecDot16 + VecDot16) - mm*SubSum(32)
+//   Q6_K          per block: 256 products summed in (half, l, q1..q4) order; sum += d*dot
+// Every product and sum is separately rounded (mul_rn / add_rn / sub_rn).
+//
+// A workgroup takes R rows and walks the columns in slabs: it stages the slab of its rows
+// and the slab of x in LDS (all loads issued before any store), computes the block terms
+// of every (row, block) in parallel, and one thread per row adds them in order.  The
+// F32/F16/BF16 lane sums are the 8R threads (row, lane), each walking its lane in order.
+// HBM-bound: every weight byte is read once per input vector.
+#include <algorithm>
+
+#include "qr_matvec.hpp"
+
+namespace qr {
+
+namespace {
+
+constexpr int kMvThreads = 256;
+constexpr int kMvSlabCols = 4096;     // x slab: 16 KiB of LDS
+constexpr int kMvTileBytes = 32768;   // weight tile per slab
+constexpr int kMvTermsPerRow = 128;   // block terms per row per slab (Q4_K: 16 blocks x 8)
+constexpr int kMvMaxRows = 16;
+constexpr int kMvStageBatch = 8;
+constexpr int kMvXLoads = kMvSlabCols / 4 / kMvThreads;
+constexpr int kMvTermStride = kMvTermsPerRow + 1;  // padded: the summing threads read distinct banks
+constexpr int kMvPersistMaxCols = 16384;           // persistent form: x of up to 16K values in LDS
+constexpr int kMvPersistXLoads = kMvPersistMaxCols / 4 / kMvThreads;
+
+// x sits in LDS in groups of 32 values 36 words apart: every group starts 16-byte aligned
+// (float4 reads) and threads reading the same offset of different groups hit different
+// banks.  xwords: LDS words for the first n values.
+constexpr int kXGroup = 36;
+__device__ __forceinline__ int xpad(int k) { return k + 4 * (k >> 5); }
+__host__ __device__ constexpr int xwords(int n) { return (n / 32 + 1) * kXGroup; }
+
+// the 32 values of the group at xg (16-byte aligned LDS) into registers
+__device__ __forceinline__ void load_group(const float* xg, float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 f = reinterpret_cast<const float4*>(xg)[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+    }
+}
+
+template <int FMT>
+struct MvFormat {
+    static constexpr bool fp = FMT == QR_FMT_F32 || FMT == QR_FMT_F16 || FMT == QR_FMT_BF16;
+    static constexpr int terms = FMT == QR_FMT_Q4_K ? 8 : 1;  // terms per block
+};
+
+struct MvLayout {
+    int R;            // rows per workgroup
+    int slab_cols;
+    int stride;       // bytes per staged row (16-byte multiple, padded)
+    int copy_bytes;   // 16, 4 or 2
+    int persistent;   // one slab, 16-byte copies, one batch per tile: matvec_persistent
+    int tstride;      // floats per row of the term buffer (persistent form; a multiple of 4)
+    __host__ __device__ size_t lds_bytes() const {
+        if (persistent)  // x rounded to whole float4 so that the term rows stay 16-byte aligned
+            return static_cast<size_t>(R) * stride + static_cast<size_t>(xwords(slab_cols)) * 4 +
+                   static_cast<size_t>(R) * tstride * 4 + static_cast<size_t>(slab_cols / 32) * 4;
+        return static_cast<size_t>(R) * stride + static_cast<size_t>(xwords(slab_cols)) * 4 +
+               static_cast<size_t>(R) * kMvTermStride * 4 + kMvTermsPerRow * 4;
+    }
+};
+
+template <int G> struct MvWord;
+template <> struct MvWord<16> { typedef u32x4_t type; };
+template <> struct MvWord<4> { typedef uint32_t type; };
+template <> struct MvWord<2> { typedef uint16_t type; };
+
+__device__ __forceinline__ float hsum8(const float (&v)[8]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = add_rn(s, v[i]);
+    return s;
+}
+
+// DotKernels.cs:86-100 (HalfBitsToFloat): exact for finite halves; exponent 31 is
+// re-biased like a normal exponent instead of becoming inf/NaN.
+__device__ __forceinline__ float f16_dot_decode(uint32_t h) {
+    if (((h >> 10) & 0x1Fu) == 0x1Fu) return __uint_as_float(((h & 0x8000u) << 16) | (143u << 23) | ((h & 0x3FFu) << 13));
+    return f16_bits_to_f32(static_cast<uint16_t>(h));
+}
+
+__device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// ---- block terms: the block at p (LDS or global memory), x of the block at xb (padded LDS)
+
+// DotKernels.cs:183-230; xg: the block's x group (LDS)
+__device__ __forceinline__ float term_q8_0(const uint8_t* p, const float* xg) {
+    float xv[32];
+    load_group(xg, xv);
+    const float d = f16_bits_to_f32(static_cast<uint16_t>(ld16(p)));
+    float acc[8];
+#pragma unroll
+    for (int L = 0; L < 8; ++L) acc[L] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int L = 0; L < 8; L += 2) {
+            const uint32_t v = ld16(p + 2 + 8 * k + L);
+            const float q0 = static_cast<float>(static_cast<int8_t>(v & 0xFFu));
+            const float q1 = static_cast<float>(static_cast<int8_t>(v >> 8));
+            acc[L] = add_rn(acc[L], mul_rn(q0, xv[8 * k + L]));
+            acc[L + 1] = add_rn(acc[L + 1], mul_rn(q1, xv[8 * k + L + 1]));
+        }
+    }
+    return mul_rn(d, hsum8(acc));
+}
+
+// DotKernels.cs:134-178; sum_x = HSum of the x lanes (precomputed per block)
+__device__ __forceinline__ float term_q4_0(const uint8_t* p, const float* xg, float sum_x) {
+    float xv[32];
+    load_group(xg, xv);
+    const float d = f16_bits_to_f32(static_cast<uint16_t>(ld16(p)));
+    float acc[8];
+#pragma unroll
+    for (int L = 0; L < 8; L += 2) {
+        const uint32_t b0 = ld16(p + 2 + L), b1 = ld16(p + 2 + 8 + L);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t v0 = (b0 >> (8 * e)) & 0xFFu, v1 = (b1 >> (8 * e)) & 0xFFu;
+            float a = 0.0f;
+            a = add_rn(a, mul_rn(static_cast<float>(v0 & 15u), xv[L + e]));
+            a = add_rn(a, mul_rn(static_cast<float>(v1 & 15u), xv[8 + L + e]));
+            a = add_rn(a, mul_rn(static_cast<float>(v0 >> 4), xv[16 + L + e]));
+            a = add_rn(a, mul_rn(static_cast<float>(v1 >> 4), xv[24 + L + e]));
+            acc[L + e] = a;
+        }
+    }
+    const float dotq = hsum8(acc);
+    return sub_rn(mul_rn(d, dotq), mul_rn(mul_rn(8.0f, d), sum_x));
+}
+
+// DotKernels.cs:361-373 (VecDot16) over 16 nibbles of bytes q[0..15] (shift 0/4) and the
+// 16 values x[0..15] (registers)
+__device__ __forceinline__ float vecdot16(const uint32_t (&q)[4], int sh, const float* x) {
+    float acc[8];
+#pragma unroll
+    for (int L = 0; L < 8; ++L) {
+        const float q0 = static_cast<float>((q[L >> 2] >> (8 * (L & 3) + sh)) & 15u);
+        const float q1 = static_cast<float>((q[2 + (L >> 2)] >> (8 * (L & 3) + sh)) & 15u);
+        acc[L] = add_rn(mul_rn(q0, x[L]), mul_rn(q1, x[8 + L]));
+    }
+    return hsum8(acc);
+}
+
+// DotKernels.cs:322-358: terms 2j and 2j+1 of one Q4_K block (the even sub-block over the
+// low nibbles of bytes 32j..32j+31, the odd one over their high nibbles); xb: the block's
+// first x group (LDS)
+__device__ __forceinline__ void terms_q4_k_pair(const uint8_t* p, int j, const float* xb, const float* subsum,
+                                                float* out) {
+    float xv[2][32];
+    load_group(xb + kXGroup * (2 * j), xv[0]);
+    load_group(xb + kXGroup * (2 * j + 1), xv[1]);
+    const u32x4_t h = *reinterpret_cast<const u32x4_t*>(p);
+    const u32x4_t qa = *reinterpret_cast<const u32x4_t*>(p + 16 + 32 * j);
+    const u32x4_t qb = *reinterpret_cast<const u32x4_t*>(p + 32 + 32 * j);
+    const float d = f16_bits_to_f32(static_cast<uint16_t>(h.x & 0xFFFFu));
+    const float dmin = f16_bits_to_f32(static_cast<uint16_t>(h.x >> 16));
+    auto byte = [&](int i) {
+        const uint32_t w = i < 4 ? h.y : i < 8 ? h.z : h.w;
+        return static_cast<int>((w >> (8 * (i & 3))) & 0xFFu);
+    };
+    const uint32_t lo[4] = {qa.x, qa.y, qa.z, qa.w};
+    const uint32_t hi[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+    for (int odd = 0; odd < 2; ++odd) {
+        const int sub = 2 * j + odd;
+        int sc, m;
+        if (sub < 4) {
+            sc = byte(sub) & 63;
+            m = byte(sub + 4) & 63;
+        } else {
+            sc = (byte(sub + 4) & 0xF) | ((byte(sub - 4) >> 6) << 4);
+            m = (byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4);
+        }
+        const float a = mul_rn(d, static_cast<float>(sc)), mm = mul_rn(dmin, static_cast<float>(m));
+        const float v = add_rn(vecdot16(lo, 4 * odd, xv[odd]), vecdot16(hi, 4 * odd, xv[odd] + 16));
+        out[odd] = sub_rn(mul_rn(a, v), mul_rn(mm, subsum[sub]));
+    }
+}
+
+// all 8 terms of a Q4_K block, sub-blocks in order
+__device__ __forceinline__ void terms_q4_k(const uint8_t* p, const float* xb, const float* subsum, float* out) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) terms_q4_k_pair(p, j, xb, subsum, out + 2 * j);
+}
+
+// DotKernels.cs:420-447; xb: the block's first x group (LDS).  Half n, lane-sum step l
+// uses x[128n + 32m + l] for m = 0..3, i.e. offset l of groups 4n+m.
+__device__ __forceinline__ float term_q6_k(const uint8_t* p, const float* xb) {
+    const float d = f16_bits_to_f32(static_cast<uint16_t>(ld16(p + 208)));
+    float dot = 0.0f;
+    for (int n = 0; n < 2; ++n) {
+        int sc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const uint32_t v = ld16(p + 192 + 8 * n + i);
+            sc[i] = static_cast<int8_t>(v & 0xFFu);
+            sc[i + 1] = static_cast<int8_t>(v >> 8);
+        }
+        const uint8_t* ql = p + 64 * n;
+        const uint8_t* qh = p + 128 + 32 * n;
+        for (int l0 = 0; l0 < 32; l0 += 8) {
+            float xv[4][8];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const float4* g = reinterpret_cast<const float4*>(xb + kXGroup * (4 * n + m) + l0);
+                const float4 f0 = g[0], f1 = g[1];
+                xv[m][0] = f0.x; xv[m][1] = f0.y; xv[m][2] = f0.z; xv[m][3] = f0.w;
+                xv[m][4] = f1.x; xv[m][5] = f1.y; xv[m][6] = f1.z; xv[m][7] = f1.w;
+            }
+#pragma unroll
+            for (int l = 0; l < 8; l += 2) {
+                const int ll = l0 + l;
+                const uint32_t la = ld16(ql + ll), lb = ld16(ql + 32 + ll), hh = ld16(qh + ll);
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int is = (ll + e) >> 4;
+                    const uint32_t a = (la >> (8 * e)) & 0xFFu, b = (lb >> (8 * e)) & 0xFFu, hb = (hh >> (8 * e)) & 0xFFu;
+                    const int q1 = static_cast<int>((a & 15u) | (((hb >> 0) & 3u) << 4));
+                    const int q2 = static_cast<int>((b & 15u) | (((hb >> 2) & 3u) << 4));
+                    const int q3 = static_cast<int>((a >> 4) | (((hb >> 4) & 3u) << 4));
+                    const int q4 = static_cast<int>((b >> 4) | (((hb >> 6) & 3u) << 4));
+                    dot = add_rn(dot, mul_rn(static_cast<float>(sc[is + 0] * (q1 - 32)), xv[0][l + e]));
+                    dot = add_rn(dot, mul_rn(static_cast<float>(sc[is + 2] * (q2 - 32)), xv[1][l + e]));
+                    dot = add_rn(dot, mul_rn(static_cast<float>(sc[is + 4] * (q3 - 32)), xv[2][l + e]));
+                    dot = add_rn(dot, mul_rn(static_cast<float>(sc[is + 6] * (q4 - 32)), xv[3][l + e]));
+                }
+            }
+        }
+    }
+    return mul_rn(d, dot);
+}
+
+// fp weight k of a staged row
+template <int FMT>
+__device__ __forceinline__ float fp_weight(const uint8_t* row, int k) {
+    if constexpr (FMT == QR_FMT_F32) return *reinterpret_cast<const float*>(row + 4 * k);
+    else if constexpr (FMT == QR_FMT_BF16) return __uint_as_float(ld16(row + 2 * k) << 16);
+    else return f16_dot_decode(ld16(row + 2 * k));
+}
+
+// Copies bytes [0, bytes) of nrows rows (row r at src + r*row_bytes) into LDS rows of
+// `stride` bytes: one batch of loads per thread is issued before its stores (indices
+// past the end clamped to a valid address, not stored).
+template <int G>
+__device__ __forceinline__ void mv_stage(const uint8_t* src, long long row_bytes, int bytes, int nrows,
+                                         uint8_t* lds, int stride, const float* xsrc, float* xlds, int xcols) {
+    typedef typename MvWord<G>::type V;
+    const int per_row = bytes / G;
+    const int total = per_row * nrows;
+    const int nx = xcols / 4;  // float4 of x
+    for (int base = 0; base < total || base == 0; base += kMvThreads * kMvStageBatch) {
+        V v[kMvStageBatch];
+        int dst[kMvStageBatch];
+#pragma unroll
+        for (int s = 0; s < kMvStageBatch; ++s) {
+            const int idx = base + threadIdx.x + s * kMvThreads;
+            const int i = min(idx, total - 1);
+            const int r = i / per_row, e = i - r * per_row;
+            v[s] = *reinterpret_cast<const V*>(src + r * row_bytes + e * G);
+            dst[s] = idx < total ? r * stride + e * G : -1;
+        }
+        if (base == 0) {  // the x slab: at most kMvSlabCols / 4 float4, issued with the first batch
+            float4 xv[kMvXLoads];
+#pragma unroll
+            for (int s = 0; s < kMvXLoads; ++s)
+                xv[s] = reinterpret_cast<const float4*>(xsrc)[min(static_cast<int>(threadIdx.x) + s * kMvThreads, nx - 1)];
+#pragma unroll
+            for (int s = 0; s < kMvXLoads; ++s) {
+                const int i = static_cast<int>(threadIdx.x) + s * kMvThreads;
+                if (i < nx) {
+                    float* d = xlds + xpad(4 * i);
+                    d[0] = xv[s].x;
+                    d[1] = xv[s].y;
+                    d[2] = xv[s].z;
+                    d[3] = xv[s].w;
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kMvStageBatch; ++s)
+            if (dst[s] >= 0) *reinterpret_cast<V*>(lds + dst[s]) = v[s];
+        if (total <= kMvThreads * kMvStageBatch) break;
+    }
+}
+
+template <int FMT, int G>
+__device__ __forceinline__ void matvec_body(const MatVecArgs& a, const MvLayout& L, uint8_t* lds) {
+    constexpr bool kFp = MvFormat<FMT>::fp;
+    constexpr int T = MvFormat<FMT>::terms;
+    FormatSpec fs;
+    weight_format_spec(FMT, &fs);
+    uint8_t* wt = lds;
+    float* xs = reinterpret_cast<float*>(lds + L.R * L.stride);
+    float* terms = xs + xwords(L.slab_cols);
+    float* aux = terms + L.R * kMvTermStride;
+    const long long r0 = static_cast<long long>(blockIdx.x) * L.R;
+    const int nrows = static_cast<int>(min(static_cast<long long>(L.R), a.rows - r0));
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    const int t = threadIdx.x;
+    const uint8_t* W = a.w + r0 * a.row_bytes;
+
+    float rowsum = 0.0f;  // Q formats: thread t < nrows
+    float acc = 0.0f;     // fp formats: thread (row t / 8, lane t % 8)
+    const int frow = min(t >> 3, nrows - 1), lane = t & 7;
+
+    for (int c0 = 0; c0 < a.cols; c0 += L.slab_cols) {
+        const int cols = min(L.slab_cols, a.cols - c0);
+        const int nbs = cols / fs.block;
+        const int sbytes = nbs * fs.bytes;
+        if (c0 > 0) __syncthreads();  // the previous slab is consumed
+        mv_stage<G>(W + static_cast<long long>(c0 / fs.block) * fs.bytes, a.row_bytes, sbytes, nrows, wt, L.stride,
+                    x + c0, xs, cols);
+        __syncthreads();
+
+        if constexpr (kFp) {
+            if ((t >> 3) < L.R) {
+                const uint8_t* row = wt + frow * L.stride;
+                for (int c = 0; c < cols; c += 64) {
+                    float wv[8], xv[8];
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) {
+                        const int k = min(c + 8 * s, cols - 8) + lane;
+                        wv[s] = fp_weight<FMT>(row, k);
+                        xv[s] = xs[xpad(k)];
+                    }
+#pragma unroll
+                    for (int s = 0; s < 8; ++s)
+                        if (c + 8 * s < cols) acc = add_rn(acc, mul_rn(wv[s], xv[s]));
+                }
+            }
+        } else {
+            // x-only block sums
+            if constexpr (FMT == QR_FMT_Q4_0) {
+                for (int i = t; i < nbs; i += kMvThreads) {
+                    const float* xb = xs + kXGroup * i;
+                    float ax[8];
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) {
+                        float s = 0.0f;
+                        s = add_rn(s, xb[l]);
+                        s = add_rn(s, xb[8 + l]);
+                        s = add_rn(s, xb[16 + l]);
+                        s = add_rn(s, xb[24 + l]);
+                        ax[l] = s;
+                    }
+                    aux[i] = hsum8(ax);
+                }
+                __syncthreads();
+            } else if constexpr (FMT == QR_FMT_Q4_K) {
+                for (int i = t; i < nbs * 8; i += kMvThreads) {
+                    const float* xg = xs + kXGroup * i;
+                    float v[32];
+#pragma unroll
+                    for (int k = 0; k < 32; ++k) v[k] = xg[k];
+                    float s = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 32; ++k) s = add_rn(s, v[k]);
+                    aux[i] = s;
+                }
+                __syncthreads();
+            }
+            // rows vary fastest: threads of one block read the same x (broadcast)
+            for (int i = t; i < nrows * nbs; i += kMvThreads) {
+                const int blk = i / nrows, row = i - blk * nrows;
+                const uint8_t* p = wt + row * L.stride + blk * fs.bytes;
+                float* out = terms + row * kMvTermStride + blk * T;
+                if constexpr (FMT == QR_FMT_Q8_0) out[0] = term_q8_0(p, xs + kXGroup * blk);
+                else if constexpr (FMT == QR_FMT_Q4_0) out[0] = term_q4_0(p, xs + kXGroup * blk, aux[blk]);
+                else if constexpr (FMT == QR_FMT_Q4_K) terms_q4_k(p, xs + kXGroup * 8 * blk, aux + 8 * blk, out);
+                else out[0] = term_q6_k(p, xs + kXGroup * 8 * blk);
+            }
+            __syncthreads();
+            if (t < nrows) {  // in order, reading 16 terms per batch
+                const float* tr = terms + t * kMvTermStride;
+                const int nt = nbs * T;
+                for (int j = 0; j < nt; j += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) v[k] = tr[min(j + k, nt - 1)];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k)
+                        if (j + k < nt) rowsum = add_rn(rowsum, v[k]);
+                }
+            }
+        }
+    }
+
+    float* y = a.y + static_cast<long long>(q) * a.rows + r0;
+    if constexpr (kFp) {
+        // HSum in lane order over the 8 consecutive threads of a row
+        const int base = (threadIdx.x & 63) & ~7;
+        float s = 0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) s = add_rn(s, __shfl(acc, base + l, 64));
+        if (lane == 0 && (t >> 3) < nrows) y[t >> 3] = s;
+    } else {
+        if (t < nrows) y[t] = rowsum;
+    }
+}
+
+// Persistent form of matvec_body for one slab (cols <= kMvSlabCols) and 16-byte
+// staging of at most one batch per tile: x and its block sums are staged once per
+// workgroup, and the loads of tile i+grid are held in registers while tile i is computed.
+template <int FMT>
+__device__ __forceinline__ void matvec_persistent(const MatVecArgs& a, const MvLayout& L, uint8_t* lds) {
+    typedef u32x4_t V;
+    constexpr int T = MvFormat<FMT>::terms;
+    constexpr int UPB = FMT == QR_FMT_Q4_K ? 4 : 1;  // work items per block (Q4_K: sub-block pairs)
+    FormatSpec fs;
+    weight_format_spec(FMT, &fs);
+    uint8_t* wt = lds;
+    float* xs = reinterpret_cast<float*>(lds + L.R * L.stride);
+    float* terms = xs + xwords(L.slab_cols);
+    float* aux = terms + L.R * L.tstride;
+    const int t = threadIdx.x;
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    const int nbs = a.cols / fs.block;
+    const int per_row = nbs * fs.bytes / 16;
+    const long long ntiles = (a.rows + L.R - 1) / L.R;
+
+    V v[kMvStageBatch];
+    int dst[kMvStageBatch];
+    auto load_tile = [&](long long it) {
+        const long long r0 = it * L.R;
+        const int nrows = static_cast<int>(min(static_cast<long long>(L.R), a.rows - r0));
+        const int total = per_row * nrows;
+        const uint8_t* src = a.w + r0 * a.row_bytes;
+#pragma unroll
+        for (int s = 0; s < kMvStageBatch; ++s) {
+            const int idx = t + s * kMvThreads;
+            const int i = min(idx, total - 1);
+            const int r = i / per_row, e = i - r * per_row;
+            v[s] = *reinterpret_cast<const V*>(src + r * a.row_bytes + e * 16);
+            dst[s] = idx < total ? r * L.stride + e * 16 : -1;
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int s = 0; s < kMvStageBatch; ++s)
+            if (dst[s] >= 0) *reinterpret_cast<V*>(wt + dst[s]) = v[s];
+    };
+
+    long long it = blockIdx.x;
+    if (it < ntiles) load_tile(it);
+    {  // x, padded, with the first tile's loads in flight
+        float4 xv[kMvPersistXLoads];
+        const int nx = a.cols / 4;
+#pragma unroll
+        for (int s = 0; s < kMvPersistXLoads; ++s)
+            xv[s] = reinterpret_cast<const float4*>(x)[min(t + s * kMvThreads, nx - 1)];
+#pragma unroll
+        for (int s = 0; s < kMvPersistXLoads; ++s) {
+            const int i = t + s * kMvThreads;
+            if (i < nx) {
+                float* d = xs + xpad(4 * i);
+                d[0] = xv[s].x;
+                d[1] = xv[s].y;
+                d[2] = xv[s].z;
+                d[3] = xv[s].w;
+            }
+        }
+    }
+    if (it < ntiles) store_tile();
+    __syncthreads();
+    if constexpr (FMT == QR_FMT_Q4_0) {
+        for (int i = t; i < nbs; i += kMvThreads) {
+            const float* xb = xs + kXGroup * i;
+            float ax[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                float sx = 0.0f;
+                sx = add_rn(sx, xb[l]);
+                sx = add_rn(sx, xb[8 + l]);
+                sx = add_rn(sx, xb[16 + l]);
+                sx = add_rn(sx, xb[24 + l]);
+                ax[l] = sx;
+            }
+            aux[i] = hsum8(ax);
+        }
+        __syncthreads();
+    } else if constexpr (FMT == QR_FMT_Q4_K) {
+        for (int i = t; i < nbs * 8; i += kMvThreads) {
+            const float* xg = xs + kXGroup * i;
+            float vv[32];
+#pragma unroll
+            for (int k = 0; k < 32; ++k) vv[k] = xg[k];
+            float sx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) sx = add_rn(sx, vv[k]);
+            aux[i] = sx;
+        }
+        __syncthreads();
+    }
+
+    for (; it < ntiles; it += gridDim.x) {
+        const long long next = it + gridDim.x;
+        if (next < ntiles) load_tile(next);  // in flight while this tile is computed
+        const long long r0 = it * L.R;
+        const int nrows = static_cast<int>(min(static_cast<long long>(L.R), a.rows - r0));
+        const int nitems = nrows * nbs * UPB;
+        for (int i = t; i < nitems; i += kMvThreads) {
+            const int unit = i / nrows, row = i - unit * nrows;  // rows vary fastest
+            const int blk = unit / UPB;
+            const uint8_t* p = wt + row * L.stride + blk * fs.bytes;
+            float* out = terms + row * L.tstride + blk * T;
+            if constexpr (FMT == QR_FMT_Q8_0) out[0] = term_q8_0(p, xs + kXGroup * blk);
+            else if constexpr (FMT == QR_FMT_Q4_0) out[0] = term_q4_0(p, xs + kXGroup * blk, aux[blk]);
+            else if constexpr (FMT == QR_FMT_Q4_K) {
+                const int j = unit - blk * UPB;
+                terms_q4_k_pair(p, j, xs + kXGroup * 8 * blk, aux + 8 * blk, out + 2 * j);
+            } else out[0] = term_q6_k(p, xs + kXGroup * 8 * blk);
+        }
+        __syncthreads();
+        if (t < nrows) {  // in order, 64 terms (16 float4 reads) per batch
+            const float4* tr = reinterpret_cast<const float4*>(terms + t * L.tstride);
+            const int nt = nbs * T;
+            float sum = 0.0f;
+            for (int j = 0; j < nt; j += 64) {
+                float4 vv[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) vv[k] = tr[min(j / 4 + k, (nt - 1) / 4)];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int base = j + 4 * k;
+                    if (base + 0 < nt) sum = add_rn(sum, vv[k].x);
+                    if (base + 1 < nt) sum = add_rn(sum, vv[k].y);
+                    if (base + 2 < nt) sum = add_rn(sum, vv[k].z);
+                    if (base + 3 < nt) sum = add_rn(sum, vv[k].w);
+                }
+            }
+            a.y[static_cast<long long>(q) * a.rows + r0 + t] = sum;
+        }
+        if (next < ntiles) {
+            __syncthreads();  // this tile's weights and terms are consumed
+            store_tile();
+            __syncthreads();
+        }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kMvThreads) void matvec_kernel(MatVecArgs a, MvLayout L) {
+    extern __shared__ __align__(16) uint8_t mv_lds[];
+    if constexpr (!MvFormat<FMT>::fp) {
+        if (L.persistent) {
+            matvec_persistent<FMT>(a, L, mv_lds);
+            return;
+        }
+    }
+    if (L.copy_bytes == 16) matvec_body<FMT, 16>(a, L, mv_lds);
+    else if (L.copy_bytes == 4) matvec_body<FMT, 4>(a, L, mv_lds);
+    else matvec_body<FMT, 2>(a, L, mv_lds);
+}
+
+
+MvLayout mv_layout(const MatVecArgs& a) {
+    FormatSpec fs;
+    weight_format_spec(a.fmt, &fs);
+    MvLayout L{};
+    L.slab_cols = std::min(a.cols, kMvSlabCols);
+    const int slab_bytes = L.slab_cols / fs.block * fs.bytes;
+    const bool fp = a.fmt == QR_FMT_F32 || a.fmt == QR_FMT_F16 || a.fmt == QR_FMT_BF16;
+    int R = std::max(1, std::min(kMvMaxRows, kMvTileBytes / slab_bytes));
+    if (fp) R = std::min(R, kMvThreads / 8);
+    // at least ~2 workgroups per CU when the rows allow it
+    const long long want = 512 / std::max(1, a.nq);
+    if (a.rows / want < R) R = static_cast<int>(std::max(1LL, a.rows / std::max(1LL, want)));
+    R = static_cast<int>(std::min<long long>(R, a.rows));
+    L.R = R;
+    L.stride = (slab_bytes + 15) / 16 * 16 + 16;
+    const uintptr_t base = reinterpret_cast<uintptr_t>(a.w);
+    auto aligned = [&](int g) { return base % g == 0 && a.row_bytes % g == 0 && slab_bytes % g == 0; };
+    L.copy_bytes = aligned(16) ? 16 : aligned(4) ? 4 : 2;
+    L.persistent = 0;
+    L.tstride = 0;
+    const long long row_bytes = a.row_bytes;
+    if (!fp && a.cols <= kMvPersistMaxCols && row_bytes % 16 == 0 && base % 16 == 0 &&
+        row_bytes <= static_cast<long long>(kMvThreads) * kMvStageBatch * 16) {
+        // the whole row is one slab; tiles of at most one batch of 16-byte copies, about two
+        // or more per workgroup
+        L.slab_cols = a.cols;
+        const int rbytes = static_cast<int>(row_bytes);
+        const int rmax = std::max(1, std::min(kMvMaxRows, kMvThreads * kMvStageBatch * 16 / rbytes));
+        L.R = static_cast<int>(std::max(1LL, std::min<long long>(rmax, a.rows / 1024)));
+        L.stride = (rbytes + 15) / 16 * 16 + 16;
+        L.copy_bytes = 16;
+        const int nt = a.cols / fs.block * (a.fmt == QR_FMT_Q4_K ? 8 : 1);
+        L.tstride = (nt + 3) / 4 * 4 + 4;
+        L.persistent = 1;
+    }
+    return L;
+}
+
+template <int FMT>
+hipError_t launch_fmt(const MatVecArgs& a, hipStream_t stream) {
+    const MvLayout L = mv_layout(a);
+    static bool attr_set = false;  // dynamic LDS above 64 KiB must be allowed per kernel
+    if (L.lds_bytes() > 65536 && !attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_kernel<FMT>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const long long tiles = (a.rows + L.R - 1) / L.R;
+    // persistent: as many workgroups as stay resident (LDS-bound), at most two per CU
+    const long long resident = 256LL * std::max<long long>(1, std::min<long long>(2, 160 * 1024 / L.lds_bytes()));
+    const dim3 grid(static_cast<unsigned>(L.persistent ? std::min(tiles, resident) : tiles), static_cast<unsigned>(a.nq));
+    hipLaunchKernelGGL((matvec_kernel<FMT>), grid, dim3(kMvThreads), L.lds_bytes(), stream, a, L);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool matvec_shape_ok(int fmt, int cols) {
+    FormatSpec fs;
+    if (!weight_format_spec(fmt, &fs) || cols < 1 || cols % fs.block) return false;
+    const bool fp = fmt == QR_FMT_F32 || fmt == QR_FMT_F16 || fmt == QR_FMT_BF16;
+    return !fp || cols % 8 == 0;
+}
+
+hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
+    if (a.nq == 0 || a.rows == 0) return hipSuccess;
+    switch (a.fmt) {
+    case QR_FMT_F32: return launch_fmt<QR_FMT_F32>(a, stream);
+    case QR_FMT_F16: return launch_fmt<QR_FMT_F16>(a, stream);
+    case QR_FMT_BF16: return launch_fmt<QR_FMT_BF16>(a, stream);
+    case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
+    case QR_FMT_Q8_0: return launch_fmt<QR_FMT_Q8_0>(a, stream);
+    case QR_FMT_Q4_K: return launch_fmt<QR_FMT_Q4_K>(a, stream);
+    case QR_FMT_Q6_K: return launch_fmt<QR_FMT_Q6_K>(a, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace qr

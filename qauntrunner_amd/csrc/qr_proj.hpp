@@ -3,6 +3,7 @@
 #pragma once
 
 #include "qr_dequant.hpp"
+#include "qr_store.hpp"
 
 namespace qr {
 
@@ -44,4 +45,6 @@ struct qr_weight {
     int cols = 0;
     long long row_bytes = 0;
     void* dev = nullptr;
+    qr::DevBuf stage;       // x / y of the host-pointer calls
+    hipStream_t stream = nullptr;
 };

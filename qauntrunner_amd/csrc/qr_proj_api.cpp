@@ -2,6 +2,7 @@
 // W_UV projections (StreamingEngine.cs:517-529, :569-576).
 #include <new>
 
+#include "qr_matvec.hpp"
 #include "qr_proj.hpp"
 #include "qr_store.hpp"
 
@@ -70,11 +71,13 @@ int qr_weight_create(qr_weight** out, int format, long long rows, int cols, cons
     w->row_bytes = rb;
     const size_t bytes = static_cast<size_t>(rows * rb);
     hipError_t e = hipGetDevice(&w->device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&w->dev, bytes);
     if (e == hipSuccess) e = hipMemcpy(w->dev, host_bytes, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         set_error("uploading %zu weight bytes failed: %s", bytes, hipGetErrorString(e));
         if (w->dev) (void)hipFree(w->dev);
+        if (w->stream) (void)hipStreamDestroy(w->stream);
         delete w;
         return e == hipErrorOutOfMemory ? QR_ERR_OUT_OF_MEMORY : QR_ERR_HIP;
     }
@@ -85,11 +88,12 @@ int qr_weight_create(qr_weight** out, int format, long long rows, int cols, cons
 int qr_weight_destroy(qr_weight* w) {
     clear_error();
     if (!w) return QR_OK;
-    if (w->dev) {
+    {
         DeviceGuard dg(w->device);
-        (void)hipFree(w->dev);
+        if (w->dev) (void)hipFree(w->dev);
+        if (w->stream) (void)hipStreamDestroy(w->stream);
+        delete w;  // releases the staging buffer on the same device
     }
-    delete w;
     return QR_OK;
 }
 
@@ -129,6 +133,56 @@ int qr_mla_wuv_dev(const void* kvb_dev, int kvb_format, int heads, int nope, int
     a.in = u_dev;
     a.out = out_dev;
     QR_HIP(launch_mla_wuv(a, static_cast<hipStream_t>(stream)));
+    return QR_OK;
+}
+
+int qr_matvec_dev(const void* w_dev, int format, long long rows, int cols, int nq, const float* x_dev,
+                  float* y_dev, void* stream) {
+    clear_error();
+    QR_CHECK_ARG(w_dev != nullptr, "null weight pointer");
+    QR_CHECK_ARG(reinterpret_cast<uintptr_t>(w_dev) % 16 == 0, "weight pointer must be 16-byte aligned");
+    QR_CHECK_ARG(matvec_shape_ok(format, cols),
+                 "format %d cannot take rows of %d weights (whole blocks; a multiple of 8 for F32/F16/BF16)",
+                 format, cols);
+    QR_CHECK_ARG(rows >= 0 && nq >= 0, "negative rows or vector count");
+    QR_CHECK_ARG(nq <= 65535, "nq %d above 65535", nq);
+    if (rows == 0 || nq == 0) return QR_OK;
+    QR_CHECK_ARG(x_dev && y_dev, "null x / y pointer");
+    QR_CHECK_ARG(reinterpret_cast<uintptr_t>(x_dev) % 16 == 0, "x must be 16-byte aligned");
+    QR_CHECK_ARG(rows <= (1LL << 31) - 1, "rows %lld too large", rows);
+    MatVecArgs a{};
+    a.w = static_cast<const uint8_t*>(w_dev);
+    a.fmt = format;
+    a.rows = rows;
+    a.cols = cols;
+    a.row_bytes = weight_row_bytes(format, cols);
+    a.nq = nq;
+    a.x = x_dev;
+    a.y = y_dev;
+    QR_HIP(launch_matvec(a, static_cast<hipStream_t>(stream)));
+    return QR_OK;
+}
+
+int qr_matvec(const qr_weight* w, int nq, const float* x, float* y) {
+    clear_error();
+    QR_CHECK_ARG(w != nullptr, "null weight handle");
+    QR_CHECK_ARG(nq >= 0, "negative vector count");
+    if (nq == 0) return QR_OK;
+    QR_CHECK_ARG(x && y, "null x / y pointer");
+    QR_CHECK_ARG(matvec_shape_ok(w->format, w->cols),
+                 "format %d cannot take rows of %d weights (whole blocks; a multiple of 8 for F32/F16/BF16)",
+                 w->format, w->cols);
+    DeviceGuard dg(w->device);
+    qr_weight* mw = const_cast<qr_weight*>(w);  // staging only; the weights are not modified
+    const size_t xb = static_cast<size_t>(nq) * w->cols * 4, yb = static_cast<size_t>(nq) * w->rows * 4;
+    const size_t xa = (xb + 255) / 256 * 256;
+    QR_TRY(mw->stage.ensure(xa + yb));
+    float* dx = static_cast<float*>(mw->stage.get());
+    float* dy = reinterpret_cast<float*>(static_cast<char*>(mw->stage.get()) + xa);
+    QR_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, w->stream));
+    QR_TRY(qr_matvec_dev(w->dev, w->format, w->rows, w->cols, nq, dx, dy, w->stream));
+    QR_HIP(hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, w->stream));
+    QR_HIP(hipStreamSynchronize(w->stream));
     return QR_OK;
 }
 

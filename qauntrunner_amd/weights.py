@@ -15,7 +15,7 @@ import numpy as np
 from . import _lib
 from ._lib import FORMATS, check
 
-__all__ = ["Weight", "row_bytes", "format_code", "mla_q_absorb_dev", "mla_wuv_dev"]
+__all__ = ["Weight", "row_bytes", "format_code", "mla_q_absorb_dev", "mla_wuv_dev", "matvec_dev"]
 
 
 def format_code(fmt) -> int:
@@ -53,6 +53,16 @@ class Weight:
         p = ctypes.c_void_p()
         check(self._lib.qr_weight_data(self._h, ctypes.byref(p)))
         return p.value
+
+    def MatVec(self, x) -> np.ndarray:
+        """DotKernels.MatVec: y = W x for host x [cols] or [nq][cols]; returns [nq][rows] (or [rows])."""
+        xa = np.ascontiguousarray(x, dtype=np.float32)
+        nq = xa.size // self.Cols
+        if xa.size != nq * self.Cols:
+            raise ValueError(f"x must hold a multiple of {self.Cols} values")
+        y = np.empty((nq, self.Rows), np.float32)
+        check(self._lib.qr_matvec(self._h, nq, xa.ctypes.data_as(ctypes.c_void_p), y.ctypes.data_as(ctypes.c_void_p)))
+        return y if xa.ndim > 1 else y[0]
 
     def close(self):
         if getattr(self, "_h", None):
@@ -93,3 +103,10 @@ def mla_wuv_dev(kvb, fmt, heads, nope, vdim, kv_lora, u, out, stream=None) -> No
     check(_lib.load().qr_mla_wuv_dev(_dev(kvb), format_code(fmt), heads, nope, vdim, kv_lora, nq,
                                      ctypes.c_void_p(u.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                                      _stream(stream)))
+
+
+def matvec_dev(w, fmt, rows, cols, x, y, stream=None) -> None:
+    """y[b, r] = DotRow(W row r, x[b]) on device tensors (DotKernels.cs:599-633)."""
+    nq = x.numel() // cols
+    check(_lib.load().qr_matvec_dev(_dev(w), format_code(fmt), rows, cols, nq, ctypes.c_void_p(x.data_ptr()),
+                                    ctypes.c_void_p(y.data_ptr()), _stream(stream)))

@@ -379,3 +379,80 @@ def test_row_bytes_and_unsupported_formats():
     for fmt, n in ((5, 256), (8, 64), (quant.FMT["Q8_0"], 48), (quant.FMT["Q4_K"], 128)):
         with pytest.raises(ValueError):
             oracle.row_bytes(fmt, n)
+
+
+# ------------------------------------------------------------------ fused dequant + dot (DotRow)
+@pytest.mark.parametrize("name", ["Q8_0", "Q6_K", "Q4_0", "Q4_K"])
+def test_dot_row_matches_dequantized_dot(name):
+    """Tests/Program.cs:129-165 (DotMatches): DotRow of each row against the dequantized
+    row dotted in fp32, relative error <= 2e-4 (12 rows, 4 blocks each)."""
+    f = quant.FMT[name]
+    bs = quant.BLOCK[f][0]
+    cols, rows = bs * 4, 12
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((rows, cols)) * 0.4).astype(F32)
+    x = (rng.standard_normal(cols) * 0.5).astype(F32)
+    raw = quant.quantize(f, w)
+    wd = oracle.dequant_rows(f, raw, cols)
+    y = oracle.matvec(f, raw, cols, x)
+    for r in range(rows):
+        s = np.float32(0)
+        for c in range(cols):
+            s = np.float32(s + np.float32(wd[r, c] * x[c]))
+        assert abs(y[r] - s) / max(abs(s), 1e-3) <= 2e-4, (name, r, y[r], s)
+
+
+@pytest.mark.parametrize("name", ["F32", "F16", "BF16"])
+def test_dot_row_fp_lane_order(name):
+    """SimdMath.DotF32 lane structure: +1e8 and -1e8 in the same lane cancel exactly before
+    the +1 of another lane is added (a sequential sum would lose the 1)."""
+    f = quant.FMT[name]
+    x = np.zeros(16, F32)
+    x[0], x[1], x[8] = 1e8, 1.0, -1e8
+    w = np.ones((1, 16), F32)
+    assert oracle.matvec(f, quant.quantize(f, w), 16, x)[0] == 1.0
+    x2 = x.copy()
+    x2[9] = -1e8                      # same lane as x[1]: lane 1 = 1 - 1e8 = -1e8
+    x2[0] = 1e8
+    assert oracle.matvec(f, quant.quantize(f, w), 16, x2)[0] == np.float32(np.float32(1e8 - 1e8) - 1e8 + 0)
+
+
+def test_dot_row_f16_exponent_31_is_finite():
+    """DotKernels.cs:86-100: the vector half converter re-biases exponent 31 like a normal
+    exponent (inf 0x7C00 -> 65536, 0x7E00 -> 98304) instead of producing inf/NaN; the scalar
+    tail (cols % 8) and the dequantizer keep the exact conversion."""
+    w = np.zeros((1, 8), np.uint16)
+    w[0, 0], w[0, 3] = 0x7C00, 0x7E00
+    x = np.zeros(8, F32)
+    x[0], x[3] = 1.0, 2.0
+    y = oracle.matvec(quant.FMT["F16"], w.view(np.uint8), 8, x)[0]
+    assert y == 65536.0 + 2 * 98304.0
+    assert np.isinf(oracle.dequant_rows(quant.FMT["F16"], w.view(np.uint8), 8)[0, 0])
+
+
+def test_dot_row_q8_0_lane_structure():
+    """Q8_0 (DotKernels.cs:183-230): lane L sums q[L], q[8+L], q[16+L], q[24+L]; blocks add in order."""
+    raw = np.zeros((1, 34), np.uint8)
+    raw[0, 0:2] = np.float16(1.0).reshape(1).view(np.uint8)
+    raw[0, 2 + np.array([0, 1, 8])] = 1
+    x = np.zeros(32, F32)
+    x[0], x[1], x[8] = 1e8, 1.0, -1e8
+    assert oracle.matvec(quant.FMT["Q8_0"], raw, 32, x)[0] == 1.0
+
+
+def test_dot_row_q4_k_order_of_terms():
+    """Q4_K (DotKernels.cs:322-358): sum += a*(VecDot16 + VecDot16) - mm*SubSum, sub-blocks in
+    order; with one sub-block scale 1 and min 0, the row is a plain lane-structured dot."""
+    sc = np.zeros(8, int)
+    mn = np.zeros(8, int)
+    sc[0] = 1
+    q = np.zeros(256, int)
+    q[[0, 1, 8]] = 1
+    blk = quant.build_q4k_block(1.0, 0.0, sc, mn, q)
+    x = np.zeros(256, F32)
+    x[0], x[1], x[8] = 1e8, 1.0, -1e8
+    assert oracle.matvec(quant.FMT["Q4_K"], blk, 256, x)[0] == 1.0
+    mn[1] = 2                       # odd sub-block: -dmin*2*SubSum(x[32:64])
+    x[32:64] = 0.5
+    blk = quant.build_q4k_block(1.0, 0.25, sc, mn, q)
+    assert oracle.matvec(quant.FMT["Q4_K"], blk, 256, x)[0] == np.float32(1.0 - 0.5 * 16.0)
