@@ -74,7 +74,12 @@ WORKLOADS = {
                          desc="the f3-matvec-q4k projections with Q8_0 weights"),
     "f3-matvec-f16": dict(kind="matvec", wfmt="F16", dtype="f32", B=1,
                           desc="the f3-matvec-q4k projections with F16 weights"),
+    "f4-stream-q4k": dict(kind="stream", wfmt="Q4_K", layers=8, budget=160 << 20, dtype="f32", B=1,
+                          desc="weight streaming: 8 llama-3-8b-shape Q4_K layers (wq, wk, wv, wo, gate, up, down "
+                               "and two norms) read from a .qw file in the page cache through the two HBM "
+                               "prefetch slots, each layer's 7 MatVecs for one token queued behind its upload"),
 }
+PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 # llama-3-8b layer projections (rows, cols): wq, wk, wv, wo, gate, up, down
 MATVEC_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096), (14336, 4096),
@@ -85,6 +90,49 @@ W_FORMATS = {"F16": (1, 1, 2), "Q8_0": (4, 32, 34), "Q4_K": (6, 256, 144)}  # co
 def matvec_bytes(w):
     code, bs, bb = W_FORMATS[w["wfmt"]]
     return sum(r * (c // bs) * bb + c * 4 + r * 4 for r, c in MATVEC_SHAPES)
+
+
+STREAM_NAMES = ["wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"]  # MATVEC_SHAPES order
+
+
+def stream_layer_bytes(w):
+    code, bs, bb = W_FORMATS[w["wfmt"]]
+    return sum(r * (c // bs) * bb for r, c in MATVEC_SHAPES)
+
+
+def write_stream_model(w, path):
+    """The f4 .qw file: per layer attn_norm, wq, wk, wv, wo, ffn_norm, gate, up, down in the
+    reference's plan order, random quant bytes under the fixed scales of synth_weights."""
+    import numpy as np
+
+    from qauntrunner_amd.store import ModelStoreBuilder
+
+    code, bs, bb = W_FORMATS[w["wfmt"]]
+    rng = np.random.default_rng(11)
+    b = ModelStoreBuilder(path, {"arch": "llama", "dim": 4096, "layers": w["layers"], "ffn": 14336})
+    plan = {}
+    for l in range(w["layers"]):
+        for k, (r, c) in enumerate(MATVEC_SHAPES):
+            if k == 0:
+                plan[f"l{l}.attn_norm"] = ((4096,), 0, 4096 * 4)
+            if k == 4:
+                plan[f"l{l}.ffn_norm"] = ((4096,), 0, 4096 * 4)
+            plan[f"l{l}.{STREAM_NAMES[k]}"] = ((r, c), code, r * (c // bs) * bb)
+    for name, (dims, fmt, size) in plan.items():
+        b.Plan(name, dims, fmt, size)
+
+    def body(name):
+        dims, fmt, size = plan[name]
+        if fmt == 0:
+            return np.ones(dims[0], np.float32).view(np.uint8)
+        raw = rng.integers(0, 256, (size // bb, bb), dtype=np.uint8)
+        if w["wfmt"] == "Q8_0":
+            raw[:, 0:2] = np.float16(0.05 / 127).reshape(1).view(np.uint8)
+        else:
+            raw[:, 0:2] = np.float16(0.05 / 15 / 32).reshape(1).view(np.uint8)
+            raw[:, 2:4] = np.float16(0.05 / 63).reshape(1).view(np.uint8)
+        return raw.reshape(-1)
+    b.Commit(body)
 
 
 KVB_FORMATS = {"F32": (0, 1, 4), "F16": (1, 1, 2), "BF16": (2, 1, 2), "Q8_0": (4, 32, 34)}  # code, block, bytes
@@ -124,6 +172,9 @@ def algorithmic(w):
     if w["kind"] == "matvec":
         # every weight byte once + x in + y out per matrix; 2 flops per weight
         return matvec_bytes(w), sum(2 * r * c for r, c in MATVEC_SHAPES)
+    if w["kind"] == "stream":
+        # the weight bytes staged from the file per forward (norms stay unstaged), 2 flops per weight
+        return w["layers"] * stream_layer_bytes(w), w["layers"] * sum(2 * r * c for r, c in MATVEC_SHAPES)
     if w["kind"] == "mla_layer":
         # latents + every kvb row once + q in + out; the q~/u hand-offs between kernels are not counted
         width = w["kv_lora"] + w["rope_dim"]
@@ -274,6 +325,71 @@ def run_gpu(w, steps, warmup):
             def close(self):
                 pass
         handle = _NoHandle()
+    elif w["kind"] == "stream":
+        import tempfile
+
+        code = W_FORMATS[w["wfmt"]][0]
+        tmpdir = tempfile.mkdtemp(prefix="qr_stream_")
+        path = os.path.join(tmpdir, "layers.qw")
+        write_stream_model(w, path)
+        xs = [torch.randn(c, device=dev, generator=gen) for _, c in MATVEC_SHAPES]
+        ys = [torch.empty(r, device=dev) for r, _ in MATVEC_SHAPES]
+        L = w["layers"]
+
+        def forward(p):
+            """StreamingEngine.Forward's weight order (StreamingEngine.cs:225-266)."""
+            p.Begin(0)
+            for l in range(L):
+                for k, (r, c) in enumerate(MATVEC_SHAPES):
+                    wt = p.Acquire(f"l{l}.{STREAM_NAMES[k]}", l, stream)
+                    qr.matvec_dev(wt, code, r, c, xs[k], ys[k], stream=stream)
+                p.Release(l, stream)
+                if l + 1 < L:
+                    p.Begin(l + 1)
+
+        store = qr.ModelStore.Open(path)
+        pipe = qr.PrefetchPipeline(store, w["budget"])
+
+        def step(i):
+            forward(pipe)
+
+        class _Stream:
+            def close(self):
+                store.Dispose()
+                os.remove(path)
+                os.rmdir(tmpdir)
+        handle = _Stream()
+
+        def resident_and_upload(steps, warmup):
+            """The same forward with every tensor resident (the MatVecs alone), and the pinned
+            host-to-device copy rate of one layer's bytes."""
+            out = {}
+            with qr.ModelStore.Open(path) as rs:
+                rp = qr.PrefetchPipeline(rs, w["budget"])
+                rs.MakeResident()
+                for _ in range(warmup):
+                    forward(rp)
+                torch.cuda.synchronize()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                for _ in range(steps):
+                    forward(rp)
+                b.record(stream)
+                torch.cuda.synchronize()
+                out["resident_ms"] = a.elapsed_time(b) / steps
+            host = torch.empty(stream_layer_bytes(w), dtype=torch.uint8, pin_memory=True)
+            devb = torch.empty_like(host, device=dev)
+            for _ in range(3):
+                devb.copy_(host, non_blocking=True)
+            torch.cuda.synchronize()
+            a.record(stream)
+            for _ in range(10):
+                devb.copy_(host, non_blocking=True)
+            b.record(stream)
+            torch.cuda.synchronize()
+            out["h2d_GBs"] = host.numel() * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
+            out["host_read_GBs"] = host_read_rate(path, host.numpy())
+            return out
     elif w["kind"] == "rope":
         n, kvd, qd = w["n"], w["kv"] * w["D"], w["heads"] * w["D"]
         set_bytes = n * (qd + 2 * kvd) * 4
@@ -340,8 +456,46 @@ def run_gpu(w, steps, warmup):
             t1.record(stream)
             torch.cuda.synchronize()
             extra[name] = t0.elapsed_time(t1) / steps
+    if w["kind"] == "stream":
+        extra = resident_and_upload(max(1, steps // 2), max(1, warmup // 2))
+        extra.update(zip(("bytes_streamed", "wait_ms", "read_ms", "staged", "skipped"),
+                         (pipe.BytesStreamed, pipe.WaitMs, pipe.ReadMs, pipe.StagedLayers, pipe.SkippedLayers)))
     handle.close()
     return ms, wall * 1e3 / steps, kernel_ms, extra
+
+
+def host_read_rate(path, pinned, threads=16, chunk=2 << 20, repeats=5):
+    """GB/s of positional reads of the file's first len(pinned) bytes into a pinned host buffer
+    by `threads` threads in `chunk` pieces (the staging reads alone; median of `repeats`)."""
+    import threading
+
+    n = pinned.size
+    view = memoryview(pinned)
+    fd = os.open(path, os.O_RDONLY)
+    rates = []
+    try:
+        for _ in range(repeats):
+            nxt = [0]
+            lock = threading.Lock()
+
+            def work():
+                while True:
+                    with lock:
+                        i = nxt[0]
+                        nxt[0] += chunk
+                    if i >= n:
+                        return
+                    os.preadv(fd, [view[i:min(n, i + chunk)]], i)
+            pool = [threading.Thread(target=work) for _ in range(threads)]
+            t = time.perf_counter()
+            for th in pool:
+                th.start()
+            for th in pool:
+                th.join()
+            rates.append(n / (time.perf_counter() - t) / 1e9)
+    finally:
+        os.close(fd)
+    return sorted(rates)[len(rates) // 2]
 
 
 def synth_weights(fmt, rows, cols, gen, dev):
@@ -448,6 +602,8 @@ def cpu_baseline(w, budget_s=10.0):
             return qr_
         unit_fraction = sample_rows / w["n"]
         sample = f"{sample_rows} of {w['n']} positions, fp32 storage"
+    elif w["kind"] == "stream":
+        return cpu_stream_baseline(w, budget_s)
     elif w["kind"] == "matvec":
         code, bs, bb = W_FORMATS[w["wfmt"]]
         sample_rows = 32
@@ -531,6 +687,53 @@ def cpu_baseline(w, budget_s=10.0):
     }
 
 
+def cpu_stream_baseline(w, budget_s):
+    """The reference's CPU forward over streamed weights, per layer: ReadLayer's positional reads
+    of the layer into one host buffer (PrefetchPipeline.cs:146-153, one thread, page cache) plus
+    DotRow over every row (sampled as in the matvec leg); the layer time times the layer count."""
+    import tempfile
+
+    import numpy as np
+
+    layer = stream_layer_bytes(w)
+    tmpdir = tempfile.mkdtemp(prefix="qr_cpu_stream_")
+    path = os.path.join(tmpdir, "layer.bin")
+    rng = np.random.default_rng(5)
+    with open(path, "wb") as f:
+        f.write(rng.integers(0, 256, layer, dtype=np.uint8).tobytes())
+    buf = bytearray(layer)
+    view = memoryview(buf)
+    fd = os.open(path, os.O_RDONLY)
+    reads = []
+    try:
+        start = time.perf_counter()
+        while time.perf_counter() - start < budget_s / 2 and len(reads) < 20:
+            t = time.perf_counter()
+            done = 0
+            while done < layer:
+                done += os.preadv(fd, [view[done:done + (64 << 20)]], done)
+            reads.append(time.perf_counter() - t)
+    finally:
+        os.close(fd)
+        os.remove(path)
+        os.rmdir(tmpdir)
+    reads.sort()
+    read_s = reads[len(reads) // 2]
+    mv = cpu_baseline(dict(w, kind="matvec"), budget_s / 2)
+    matvec_s = matvec_bytes(w) / (mv["value"] * 1e12)
+    step_s = w["layers"] * (read_s + matvec_s)
+    bytes_step, _ = algorithmic(w)
+    return {
+        "value": bytes_step / step_s / 1e12,
+        "unit": "TB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"per layer: {layer / 1e6:.1f} MB read from the page cache in {read_s * 1e3:.1f} ms "
+                   f"(median of {len(reads)}) + DotRow over all rows {matvec_s * 1e3:.1f} ms "
+                   f"({mv['sample']}); step = {w['layers']} layers, {step_s * 1e3:.1f} ms"),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -574,9 +777,18 @@ def main():
         achieved = bytes_step / (kms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
                 "frac": achieved / (HBM_PEAK_TBS * 1e3), "traffic": None}
+    if w["kind"] == "stream":
+        # the kernels of the step are the MatVecs; timed with every tensor resident
+        kms = extra["resident_ms"]
+        mv_bytes = w["layers"] * matvec_bytes(w)
+        achieved = mv_bytes / (kms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
+                "frac": achieved / (HBM_PEAK_TBS * 1e3), "traffic": None}
     roof["traffic"] = profiled_traffic(args.config)
     roof["kernel_us"] = round(kms * 1e3, 3)
     roof["kernel"] = "split-K kernel (HIP events around it)" if kernel_ms else "whole step (HIP events)"
+    if w["kind"] == "stream":
+        roof["kernel"] = f"the {7 * w['layers']} MatVecs of a resident forward (HIP events)"
     line = {
         "metric": METRIC,
         "value": round(tbs, 4),
@@ -590,12 +802,26 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
-        "data": "synthetic N(0,1) on device" + (", RoPE base 500000 on Q/K" if w.get("rope") else ""),
+        "data": ("synthetic Q4_K blocks (random quants, fixed scales) in a .qw file in the page cache"
+                 if w["kind"] == "stream" else
+                 "synthetic N(0,1) on device" + (", RoPE base 500000 on Q/K" if w.get("rope") else "")),
         "config": {"workload": w["desc"], "name": args.config, "algorithmic_bytes": bytes_step,
                    "algorithmic_flops": flops_step, "host_wall_ms_per_step": round(wall_ms, 4)},
         "roofline": roof,
     }
-    if extra:
+    if w["kind"] == "stream":
+        streamed = bytes_step / (ms * 1e-3) / 1e9
+        line["stream"] = {
+            "staged_GBs": round(streamed, 2), "peak_GBs": PCIE_PEAK_GBS, "peak": "PCIe 5.0 x16, one direction",
+            "frac": round(streamed / PCIE_PEAK_GBS, 4),
+            "h2d_pinned_GBs": round(extra["h2d_GBs"], 2),
+            "host_read_pinned_GBs": round(extra["host_read_GBs"], 2),
+            "resident_ms_per_step": round(extra["resident_ms"], 4),
+            "layer_bytes": stream_layer_bytes(w), "budget": w["budget"],
+            "host_wait_ms_total": round(extra["wait_ms"], 2), "host_read_ms_total": round(extra["read_ms"], 2),
+            "bytes_streamed_total": extra["bytes_streamed"], "staged_layers": extra["staged"],
+            "skipped_layers": extra["skipped"]}
+    elif extra:
         # the projection kernels timed alone (HIP events around `steps` launches each)
         H, nope, vdim, L = w["heads"], w["nope"], w["vdim"], w["kv_lora"]
         per_row = kvb_bytes(w) // (H * (nope + vdim))

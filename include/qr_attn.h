@@ -251,6 +251,55 @@ int qr_matvec_dev(const void* w_dev, int format, long long rows, int cols, int n
 /* Same with host vectors against an uploaded weight (synchronous; not thread-safe per weight). */
 int qr_matvec(const qr_weight* w, int nq, const float* x, float* y);
 
+/* ---------------------------------------------------------------- .qw weight files in HBM
+ * A qr_model is one opened .qw file (ModelStore) plus its layer prefetch pipeline
+ * (PrefetchPipeline).  The file stays open; tensors are read with positional reads.  Device
+ * memory is taken on the device current at the first Begin / Acquire / make_resident call.
+ * A handle is used from one host thread at a time. */
+typedef struct qr_model qr_model;
+/* ModelStore.Open, ModelStore.cs:85-126: "QWR1", int32 header length, JSON header
+ * {config, tensors[{name, dims, format, offset, size}], data_offset?}; data starts at the
+ * 64-byte-aligned data_offset (or header end).  Host only: no device call. */
+int qr_model_open(qr_model** out, const char* path);
+/* ModelStore.Dispose + PrefetchPipeline.Dispose (ModelStore.cs:128-132, PrefetchPipeline.cs:179-189):
+ * waits for pending reads, uploads and the work that acquired a slot, then frees everything. */
+int qr_model_close(qr_model* m);
+/* ModelStore.Tensors (ModelStore.cs:69): count and names in header order. */
+int qr_model_tensor_count(const qr_model* m, int* count);
+int qr_model_tensor_name(const qr_model* m, int index, char* buf, int buf_len);
+/* TensorView.Format / Dims / SizeBytes (ModelStore.cs:10-27) of ModelStore.Get(name) (:79-80). */
+int qr_model_tensor_info(const qr_model* m, const char* name, int* format, int* ndims, long long* dims,
+                         int dims_cap, long long* bytes);
+/* TensorView.Bytes (ModelStore.cs:27): the tensor's bytes into host memory. */
+int qr_model_read(const qr_model* m, const char* name, void* dst, long long dst_bytes);
+/* new PrefetchPipeline(store, budgetBytes), PrefetchPipeline.cs:52-61: 0 disables staging. */
+int qr_model_set_prefetch(qr_model* m, long long budget_bytes);
+/* PrefetchPipeline.Begin, PrefetchPipeline.cs:64-75: starts staging layer `layer` (tensors named
+ * "l<layer>.*" except those ending in "norm" or "router"; every tensor for a negative layer) into
+ * HBM slot layer & 1.  The slot's next upload waits, on the GPU, for the work queued so far on
+ * every stream that acquired the slot's previous layer: pointers of that layer are not valid
+ * for work queued after this call. */
+int qr_model_begin(qr_model* m, int layer);
+/* PrefetchPipeline.Acquire, PrefetchPipeline.cs:82-97: device address of tensor `name` as layer
+ * `layer` uses it.  Staged: `stream` waits on the GPU for the slot's upload.  Not staged (layer
+ * never begun, over budget, read failed, norms and routers, pipeline off): the tensor is uploaded
+ * once and kept, as the reference falls back to its mmap view. */
+int qr_model_acquire(qr_model* m, const char* name, int layer, void* stream, const void** dev_ptr);
+/* No counterpart in the reference (its compute is synchronous): marks the end of the work that
+ * `stream` queued on layer `layer`'s staged tensors, so the slot's next upload can start as soon
+ * as that work is done instead of waiting for everything queued before the next Begin.  Call it
+ * after the layer's last launch on each stream that acquired it; without it, Begin fences. */
+int qr_model_release(qr_model* m, int layer, void* stream);
+/* PrefetchPipeline.WaitLayer, PrefetchPipeline.cs:100-109: waits for the layer's file read. */
+int qr_model_wait_layer(qr_model* m, int layer);
+/* No counterpart in the reference: uploads every tensor once into one HBM allocation, after
+ * which Acquire serves all of them with no copy and no wait.  For models that fit in HBM. */
+int qr_model_make_resident(qr_model* m);
+/* PrefetchPipeline BytesStreamed / WaitTicks / ReadTicks / StagedLayers / SkippedLayers
+ * (PrefetchPipeline.cs:40-48), times in milliseconds. */
+int qr_model_stats(qr_model* m, long long* bytes_streamed, double* wait_ms, double* read_ms, int* staged_layers,
+                   int* skipped_layers);
+
 #ifdef __cplusplus
 }
 #endif

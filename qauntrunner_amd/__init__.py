@@ -2,7 +2,8 @@
 
 The product is the C-ABI library ``libqr_attn.so`` (include/qr_attn.h) built
 from ``csrc/``; this package holds its ctypes binding and the host-side
-mirror of the reference classes PagedKvCache and MlaLatentCache.
+mirror of the reference classes PagedKvCache, MlaLatentCache, ModelStore and
+PrefetchPipeline.
 """
 from ._lib import (
     DTYPE_BF16,
@@ -19,6 +20,7 @@ from ._lib import (
     load,
 )
 from .caches import MlaLatentCache, PagedKvCache, dtype_code
+from .store import DeviceTensor, ModelStore, ModelStoreBuilder, PrefetchPipeline, TensorView
 from .weights import Weight, matvec_dev, mla_q_absorb_dev, mla_wuv_dev
 
 __all__ = [
@@ -26,4 +28,5 @@ __all__ = [
     "QrError", "QrHipError", "QrInvalidArgument", "QrNotResident", "QrOutOfMemory", "QrOutOfRange",
     "load", "MlaLatentCache", "PagedKvCache", "dtype_code",
     "Weight", "matvec_dev", "mla_q_absorb_dev", "mla_wuv_dev",
+    "DeviceTensor", "ModelStore", "ModelStoreBuilder", "PrefetchPipeline", "TensorView",
 ]

@@ -113,6 +113,19 @@ SIGNATURES = {
     "qr_mla_wuv_dev": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     "qr_matvec_dev": [_p, _i, ctypes.c_longlong, _i, _i, _p, _p, _p],
     "qr_matvec": [_p, _i, _p, _p],
+    "qr_model_open": [_pp, ctypes.c_char_p],
+    "qr_model_close": [_p],
+    "qr_model_tensor_count": [_p, _ip],
+    "qr_model_tensor_name": [_p, _i, ctypes.c_char_p, _i],
+    "qr_model_tensor_info": [_p, ctypes.c_char_p, _ip, _ip, _llp, _i, _llp],
+    "qr_model_read": [_p, ctypes.c_char_p, _p, ctypes.c_longlong],
+    "qr_model_set_prefetch": [_p, ctypes.c_longlong],
+    "qr_model_begin": [_p, _i],
+    "qr_model_acquire": [_p, ctypes.c_char_p, _i, _p, _pp],
+    "qr_model_release": [_p, _i, _p],
+    "qr_model_wait_layer": [_p, _i],
+    "qr_model_make_resident": [_p],
+    "qr_model_stats": [_p, _llp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double), _ip, _ip],
 }
 _RESTYPES = {"qr_last_error": ctypes.c_char_p, "qr_status_name": ctypes.c_char_p}
 
