@@ -19,6 +19,7 @@
 #include <algorithm>
 
 #include "qr_matvec.hpp"
+#include "qr_mfma.hpp"
 
 namespace qr {
 
@@ -245,6 +246,270 @@ __device__ __forceinline__ float term_q6_k(const uint8_t* p, const float* xb) {
         }
     }
     return mul_rn(d, dot);
+}
+
+// ---- Q4_K, one thread per (row, sub-block pair): DotKernels.cs:322-373 with x in registers.
+// Pair pc = 4*block + j covers x[64*pc .. 64*pc+63]: sub-block 2j over the low nibbles of
+// quant bytes 32j..32j+31, sub-block 2j+1 over their high nibbles.
+
+// w & 0x0F0F0F0F, opaque to the optimiser: it would otherwise fold the mask into one
+// bit-field extract per nibble, where a byte-to-float conversion of the masked word
+// (v_cvt_f32_ubyte0..3) takes one instruction per nibble.
+__device__ __forceinline__ uint32_t nibble_mask(uint32_t w) {
+    uint32_t m;
+    asm("v_and_b32 %0, %1, %2" : "=v"(m) : "s"(0x0F0F0F0Fu), "v"(w));
+    return m;
+}
+
+// VecDot16 (DotKernels.cs:361-373) over 16 nibbles already masked into bytes: q holds bytes
+// 0..15 (the value of nibble L is byte L of q), x the 16 values
+__device__ __forceinline__ float vecdot16_bytes(const uint32_t (&q)[4], const float* x) {
+    float acc[8];
+#pragma unroll
+    for (int L = 0; L < 8; ++L) {
+        const float q0 = static_cast<float>((q[L >> 2] >> (8 * (L & 3))) & 0xFFu);
+        const float q1 = static_cast<float>((q[2 + (L >> 2)] >> (8 * (L & 3))) & 0xFFu);
+        acc[L] = add_rn(mul_rn(q0, x[L]), mul_rn(q1, x[8 + L]));
+    }
+    return hsum8(acc);
+}
+
+// the two terms of pair j of the block whose header is h, quants qa (bytes 32j..32j+15)
+// and qb (32j+16..32j+31), against x[0..63] and the two sub-block sums of x
+__device__ __forceinline__ void q4k_pair_terms(const u32x4_t h, const u32x4_t qa, const u32x4_t qb, int j,
+                                               const float (&x)[64], float ss0, float ss1, float& t0, float& t1) {
+    const float d = f16_bits_to_f32(static_cast<uint16_t>(h.x & 0xFFFFu));
+    const float dmin = f16_bits_to_f32(static_cast<uint16_t>(h.x >> 16));
+    auto byte = [&](int i) {
+        const uint32_t w = i < 4 ? h.y : i < 8 ? h.z : h.w;
+        return static_cast<int>((w >> (8 * (i & 3))) & 0xFFu);
+    };
+    const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w};
+    const uint32_t b[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+    for (int odd = 0; odd < 2; ++odd) {
+        const int sub = 2 * j + odd;
+        int sc, m;
+        if (sub < 4) {
+            sc = byte(sub) & 63;
+            m = byte(sub + 4) & 63;
+        } else {
+            sc = (byte(sub + 4) & 0xF) | ((byte(sub - 4) >> 6) << 4);
+            m = (byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4);
+        }
+        uint32_t na[4], nb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            na[i] = nibble_mask(odd ? a[i] >> 4 : a[i]);
+            nb[i] = nibble_mask(odd ? b[i] >> 4 : b[i]);
+        }
+        const float as = mul_rn(d, static_cast<float>(sc)), mm = mul_rn(dmin, static_cast<float>(m));
+        const float v = add_rn(vecdot16_bytes(na, x + 32 * odd), vecdot16_bytes(nb, x + 32 * odd + 16));
+        const float t = sub_rn(mul_rn(as, v), mul_rn(mm, odd ? ss1 : ss0));
+        if (odd) t1 = t;
+        else t0 = t;
+    }
+}
+
+// Thread (row group g, pair column pc) computes the two terms of RPT rows of pair pc; the
+// terms go to LDS and one thread per row then adds them in order.  Weight loads of all RPT
+// rows and the 64 x values are issued before any arithmetic.
+struct MvQ4k {
+    int P;        // pairs per row (cols / 64)
+    int tpg;      // threads per row group (a multiple of 64, <= 256)
+    int rg;       // row groups per workgroup
+    int R;        // rows per workgroup (rg * RPT)
+    int tstride;  // floats per LDS term row (2P rounded up to 4, plus 4)
+};
+
+template <int RPT>
+__global__ __launch_bounds__(kMvThreads) void matvec_q4k_kernel(MatVecArgs a, MvQ4k k) {
+    extern __shared__ __align__(16) uint8_t mv_lds[];
+    float* terms = reinterpret_cast<float*>(mv_lds);
+    const int t = threadIdx.x;
+    const int g = t / k.tpg;
+    const long long r0 = static_cast<long long>(blockIdx.x) * k.R;
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    if (g < k.rg) {
+        for (int pc = t - g * k.tpg; pc < k.P; pc += k.tpg) {
+            const int blk = pc >> 2, j = pc & 3;
+            u32x4_t h[RPT], qa[RPT], qb[RPT];
+#pragma unroll
+            for (int r = 0; r < RPT; ++r) {
+                const long long row = min(r0 + g * RPT + r, a.rows - 1);
+                const uint8_t* p = a.w + row * a.row_bytes + blk * 144;
+                h[r] = *reinterpret_cast<const u32x4_t*>(p);
+                qa[r] = *reinterpret_cast<const u32x4_t*>(p + 16 + 32 * j);
+                qb[r] = *reinterpret_cast<const u32x4_t*>(p + 32 + 32 * j);
+            }
+            float xv[64];
+            const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 f = x4[i];
+                xv[4 * i] = f.x;
+                xv[4 * i + 1] = f.y;
+                xv[4 * i + 2] = f.z;
+                xv[4 * i + 3] = f.w;
+            }
+            float ss0 = 0.0f, ss1 = 0.0f;  // SubSum over the 32 values of each sub-block, in order
+#pragma unroll
+            for (int i = 0; i < 32; ++i) ss0 = add_rn(ss0, xv[i]);
+#pragma unroll
+            for (int i = 32; i < 64; ++i) ss1 = add_rn(ss1, xv[i]);
+#pragma unroll
+            for (int r = 0; r < RPT; ++r) {
+                float t0, t1;
+                q4k_pair_terms(h[r], qa[r], qb[r], j, xv, ss0, ss1, t0, t1);
+                *reinterpret_cast<float2*>(terms + (g * RPT + r) * k.tstride + 2 * pc) = make_float2(t0, t1);
+            }
+        }
+    }
+    __syncthreads();
+    if (t < k.R && r0 + t < a.rows) {  // in order, 16 terms (4 float4 reads) per batch
+        const float4* tr = reinterpret_cast<const float4*>(terms + t * k.tstride);
+        const int nt = 2 * k.P;
+        float sum = 0.0f;
+        for (int i = 0; i < nt; i += 16) {
+            float4 vv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vv[c] = tr[min(i / 4 + c, (nt - 1) / 4)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int base = i + 4 * c;
+                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
+                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
+                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
+                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
+            }
+        }
+        a.y[static_cast<long long>(q) * a.rows + r0 + t] = sum;
+    }
+}
+
+// Persistent form: workgroup w takes row tiles w, w + G, w + 2G, ... (G = gridDim.x, R rows a
+// tile).  x and its sub-block sums stay in registers for all of them, the next tile's weights
+// are loaded while the current tile is computed (two register buffers, the loop unrolled by
+// two so that each half waits only for its own loads), every tile's terms stay in LDS, and the
+// in-order sums of all the workgroup's rows run at the end.  blockDim = rg * tpg threads.
+struct MvQ4kP {
+    int P, tpg, rg, R, tstride;
+    int ntiles;   // ceil(rows / R)
+};
+
+// Loads of one tile through a buffer resource made for it (uniform base and size), so that a
+// tile costs scalar arithmetic only: lane offsets vh/vq (block header, first quant vector of
+// the lane's pair, per row) are fixed for the whole kernel.  Rows past the end of the matrix
+// lie outside the resource and read as zero; their terms are never summed.
+template <int RPT>
+__device__ __forceinline__ void q4k_load(const MatVecArgs& a, const MvQ4kP& k, int tile, const uint32_t (&vh)[RPT],
+                                         const uint32_t (&vq)[RPT], u32x4_t (&h)[RPT], u32x4_t (&qa)[RPT],
+                                         u32x4_t (&qb)[RPT]) {
+    // 32-bit uniform arithmetic (rows < 2^31 and R * row_bytes < 2^31 are checked on the host):
+    // a 64-bit compare would be done in vector registers
+    const int r0 = tile * k.R;
+    const int nrec = min(k.R, static_cast<int>(a.rows) - r0) * static_cast<int>(a.row_bytes);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(a.w + static_cast<long long>(r0) * a.row_bytes), static_cast<short>(0), nrec,
+        kBufferFlags);
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        h[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vh[r], 0, 0);
+        qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vq[r], 0, 0);
+        qb[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vq[r] + 16, 0, 0);
+    }
+}
+
+template <int RPT>
+__global__ __launch_bounds__(512) void matvec_q4k_persistent(MatVecArgs a, MvQ4kP k) {
+    extern __shared__ __align__(16) uint8_t mv_lds[];
+    float* terms = reinterpret_cast<float*>(mv_lds);
+    const int t = threadIdx.x;
+    const int g = t / k.tpg;
+    const bool active = t - g * k.tpg < k.P;
+    // lanes past the row's pairs load and compute pair P-1 and store nothing: no branch
+    // around the loads, so the wait counts stay exact
+    const int pc = min(t - g * k.tpg, k.P - 1);
+    const int blk = pc >> 2, j = pc & 3;
+    const int G = gridDim.x;
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    const int last = k.ntiles - 1;
+
+    uint32_t vh[RPT], vq[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        vh[r] = static_cast<uint32_t>((g * RPT + r) * a.row_bytes + blk * 144);
+        vq[r] = vh[r] + 16 + 32 * j;
+    }
+    u32x4_t hA[RPT], qaA[RPT], qbA[RPT], hB[RPT], qaB[RPT], qbB[RPT];
+    int it = blockIdx.x;
+    q4k_load<RPT>(a, k, it, vh, vq, hA, qaA, qbA);
+    float xv[64];
+    float ss0 = 0.0f, ss1 = 0.0f;
+    {
+        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 f = x4[i];
+            xv[4 * i] = f.x;
+            xv[4 * i + 1] = f.y;
+            xv[4 * i + 2] = f.z;
+            xv[4 * i + 3] = f.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) ss0 = add_rn(ss0, xv[i]);
+#pragma unroll
+        for (int i = 32; i < 64; ++i) ss1 = add_rn(ss1, xv[i]);
+    }
+    auto compute = [&](const u32x4_t (&h)[RPT], const u32x4_t (&qa)[RPT], const u32x4_t (&qb)[RPT], int slot) {
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            float t0, t1;
+            q4k_pair_terms(h[r], qa[r], qb[r], j, xv, ss0, ss1, t0, t1);
+            if (active)
+                *reinterpret_cast<float2*>(terms + ((slot * k.R) + g * RPT + r) * k.tstride + 2 * pc) =
+                    make_float2(t0, t1);
+        }
+    };
+    int slot = 0;
+    for (;;) {  // exits only through the breaks: the back-edge is the steady state
+        const int n1 = it + G;
+        q4k_load<RPT>(a, k, min(n1, last), vh, vq, hB, qaB, qbB);
+        compute(hA, qaA, qbA, slot++);
+        if (n1 > last) break;
+        it = n1;
+        const int n2 = it + G;
+        q4k_load<RPT>(a, k, min(n2, last), vh, vq, hA, qaA, qbA);
+        compute(hB, qaB, qbB, slot++);
+        if (n2 > last) break;
+        it = n2;
+    }
+    __syncthreads();
+    // in-order sums: thread t takes row t % R of the workgroup's tile t / R
+    const int nt = 2 * k.P;
+    for (int i = t; i < slot * k.R; i += blockDim.x) {
+        const int s = i / k.R, r = i - s * k.R;
+        const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
+        if (row >= a.rows) continue;
+        const float4* tr = reinterpret_cast<const float4*>(terms + i * k.tstride);
+        float sum = 0.0f;
+        for (int c0 = 0; c0 < nt; c0 += 16) {
+            float4 vv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vv[c] = tr[min(c0 / 4 + c, (nt - 1) / 4)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int base = c0 + 4 * c;
+                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
+                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
+                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
+                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
+            }
+        }
+        a.y[static_cast<long long>(q) * a.rows + row] = sum;
+    }
 }
 
 // fp weight k of a staged row
@@ -610,6 +875,74 @@ MvLayout mv_layout(const MatVecArgs& a) {
     return L;
 }
 
+// Q4_K rows through matvec_q4k_kernel: weights and x 16-byte aligned (a Q4_K row is 144-byte
+// blocks, so rows stay aligned when the base is) and the term rows within 64 KiB of LDS.
+#ifndef QR_MV_Q4K_RPT
+#define QR_MV_Q4K_RPT 0
+#endif
+
+bool q4k_config(const MatVecArgs& a, MvQ4k* k, int* rpt_out) {
+    if (a.fmt != QR_FMT_Q4_K || reinterpret_cast<uintptr_t>(a.w) % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
+        a.row_bytes % 16)
+        return false;
+    k->P = a.cols / 64;
+    k->tpg = std::min(kMvThreads, (k->P + 63) / 64 * 64);
+    k->rg = kMvThreads / k->tpg;
+    // rows per thread: halved while that leaves fewer than 1024 workgroups
+    int rpt = 4;
+    while (rpt > 1 && (a.rows + static_cast<long long>(k->rg) * rpt - 1) / (static_cast<long long>(k->rg) * rpt) < 1024)
+        rpt >>= 1;
+    if (QR_MV_Q4K_RPT) rpt = QR_MV_Q4K_RPT;
+    k->R = k->rg * rpt;
+    k->tstride = (2 * k->P + 3) / 4 * 4 + 4;
+    *rpt_out = rpt;
+    return static_cast<size_t>(k->R) * k->tstride * 4 <= 64 * 1024;
+}
+
+#ifndef QR_MV_Q4KP_RPT
+#define QR_MV_Q4KP_RPT 2
+#endif
+#ifndef QR_MV_Q4KP_WGCU
+#define QR_MV_Q4KP_WGCU 3
+#endif
+
+// The persistent Q4_K form for rows of at most 512 pairs (32768 columns): false when the
+// terms of a workgroup's tiles would not fit in 64 KiB of LDS.
+bool q4k_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
+    if (a.fmt != QR_FMT_Q4_K || reinterpret_cast<uintptr_t>(a.w) % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
+        a.row_bytes % 16)
+        return false;
+    MvQ4kP k{};
+    k.P = a.cols / 64;
+    if (k.P > 512) return false;
+    k.tpg = (k.P + 63) / 64 * 64;
+    k.rg = std::max(1, kMvThreads / k.tpg);
+    constexpr int rpt = QR_MV_Q4KP_RPT;
+    k.R = k.rg * rpt;
+    k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
+    k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
+    if (static_cast<long long>(k.R) * a.row_bytes >= (1LL << 31) || a.rows >= (1LL << 31) - k.R) return false;
+    const int threads = k.rg * k.tpg;
+    const int wg_per_cu = std::max(1, QR_MV_Q4KP_WGCU * 256 / threads);
+    int G = std::min(k.ntiles, 256 * wg_per_cu);
+    const int tpw = (k.ntiles + G - 1) / G;
+    const size_t lds = static_cast<size_t>(tpw) * k.R * k.tstride * 4;
+    if (lds > 64 * 1024) return false;
+    const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
+    hipLaunchKernelGGL(matvec_q4k_persistent<rpt>, grid, dim3(threads), lds, stream, a, k);
+    *err = hipGetLastError();
+    return true;
+}
+
+hipError_t launch_q4k(const MatVecArgs& a, const MvQ4k& k, int rpt, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(k.R) * k.tstride * 4;
+    const dim3 grid(static_cast<unsigned>((a.rows + k.R - 1) / k.R), static_cast<unsigned>(a.nq));
+    if (rpt == 4) hipLaunchKernelGGL(matvec_q4k_kernel<4>, grid, dim3(kMvThreads), lds, stream, a, k);
+    else if (rpt == 2) hipLaunchKernelGGL(matvec_q4k_kernel<2>, grid, dim3(kMvThreads), lds, stream, a, k);
+    else hipLaunchKernelGGL(matvec_q4k_kernel<1>, grid, dim3(kMvThreads), lds, stream, a, k);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_fmt(const MatVecArgs& a, hipStream_t stream) {
     const MvLayout L = mv_layout(a);
@@ -645,7 +978,14 @@ hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
     case QR_FMT_BF16: return launch_fmt<QR_FMT_BF16>(a, stream);
     case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
     case QR_FMT_Q8_0: return launch_fmt<QR_FMT_Q8_0>(a, stream);
-    case QR_FMT_Q4_K: return launch_fmt<QR_FMT_Q4_K>(a, stream);
+    case QR_FMT_Q4_K: {
+        hipError_t e;
+        if (q4k_persistent_launch(a, stream, &e)) return e;
+        MvQ4k k;
+        int rpt;
+        if (q4k_config(a, &k, &rpt)) return launch_q4k(a, k, rpt, stream);
+        return launch_fmt<QR_FMT_Q4_K>(a, stream);
+    }
     case QR_FMT_Q6_K: return launch_fmt<QR_FMT_Q6_K>(a, stream);
     default: return hipErrorInvalidValue;
     }
