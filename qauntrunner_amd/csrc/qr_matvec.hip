@@ -512,6 +512,290 @@ __global__ __launch_bounds__(512) void matvec_q4k_persistent(MatVecArgs a, MvQ4k
     }
 }
 
+// ---- F32 / F16 / BF16 (DotF32 order, DotKernels.cs:52-100): producer/consumer workgroups.
+// Row r's lane L accumulates k = 8c + L over the chunks c in order, so every row is 8 serial
+// chains.  A workgroup takes 8 rows.  Four producer waves stream the rows in segments of 64
+// chunks (16-byte loads two segments ahead), form the products w*x and write them to LDS
+// chain-major, P[row][L][c]; the fifth wave holds the 64 chains (row, L) and adds each
+// segment in order while the producers fill the other buffer.  F16 weights are decoded with
+// v_cvt_f32_f16, exact for every half but those with exponent 31, which the reference's vector
+// converter reads as finite 2^16-scale values; such a half makes its product, hence the row,
+// non-finite, and a row whose result is not finite is recomputed with the exact decoder.
+constexpr int kFpRows = 8;
+constexpr int kFpSeg = 64;                      // chunks of 8 columns per segment
+constexpr int kFpPad = kFpSeg + 4;              // floats per (row, lane) product row: distinct banks
+constexpr int kFpProducers = 256;
+constexpr int kFpThreads = kFpProducers + 64;   // + the chain wave
+#ifndef QR_MV_FP_SLOTS
+#define QR_MV_FP_SLOTS 6
+#endif
+constexpr int kFpSlots = QR_MV_FP_SLOTS;         // register slots: loads run kFpSlots - 1 segments ahead
+
+template <int FMT> struct FpLoad {               // one row's chunk (8 weights)
+    u32x4_t w[FMT == QR_FMT_F32 ? 2 : 1];
+};
+
+// chunk cl of segment s of a row (buffer resource rs): lane offset vo = 16 cl (F32: 32 cl),
+// segment offset so uniform; chunks past the row read as zero
+template <int FMT>
+__device__ __forceinline__ void fp_load_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so, FpLoad<FMT>& l) {
+    l.w[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 0);
+    if constexpr (FMT == QR_FMT_F32) l.w[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 16, so, 0);
+}
+
+template <int FMT>
+__device__ __forceinline__ void fp_decode(const FpLoad<FMT>& l, float (&v)[8]) {
+    if constexpr (FMT == QR_FMT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __uint_as_float(l.w[0][i]);
+            v[4 + i] = __uint_as_float(l.w[1][i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = l.w[0][i];
+            if constexpr (FMT == QR_FMT_BF16) {
+                v[2 * i] = __uint_as_float(w << 16);
+                v[2 * i + 1] = __uint_as_float(w & 0xFFFF0000u);
+            } else {
+                v[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w & 0xFFFFu));
+                v[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w >> 16));
+            }
+        }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kFpThreads) void matvec_fp_kernel(MatVecArgs a) {
+    __shared__ __align__(16) float P[2][kFpRows * 8 * kFpPad];
+    const int t = threadIdx.x;
+    const long long r0 = static_cast<long long>(blockIdx.x) * kFpRows;
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    const int nch = a.cols / 8;
+    const int nseg = (nch + kFpSeg - 1) / kFpSeg;
+
+    if (t < kFpProducers) {
+        // chunk cl of every segment, rows 2pr and 2pr+1
+        // Rows 2pr and 2pr+1 are uniform in a wave: each is a buffer resource and a chunk is a
+        // lane offset plus a uniform segment offset, so the loop costs no vector address
+        // arithmetic (rows past the matrix read row rows-1 and are never stored).
+        const int cl = t & (kFpSeg - 1), pr = __builtin_amdgcn_readfirstlane(t >> 6);
+        constexpr int B = FMT == QR_FMT_F32 ? 32 : 16;
+        const int rbytes = nch * B;
+        const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(a.w + min(r0 + 2 * pr, a.rows - 1) * a.row_bytes), static_cast<short>(0), rbytes,
+            kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(a.w + min(r0 + 2 * pr + 1, a.rows - 1) * a.row_bytes), static_cast<short>(0),
+            rbytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(x), static_cast<short>(0), nch * 32, kBufferFlags);
+        const uint32_t vo = static_cast<uint32_t>(cl * B), vx = static_cast<uint32_t>(cl * 32);
+        float* out0 = &P[0][(2 * pr) * 8 * kFpPad + cl];
+        FpLoad<FMT> w0[kFpSlots], w1[kFpSlots];
+        u32x4_t xa[kFpSlots], xb[kFpSlots];
+        auto issue = [&](int s, FpLoad<FMT>& l0, FpLoad<FMT>& l1, u32x4_t& x0, u32x4_t& x1) {
+            const uint32_t so = static_cast<uint32_t>(s * kFpSeg * B), sx = static_cast<uint32_t>(s * kFpSeg * 32);
+            fp_load_chunk<FMT>(rs0, vo, so, l0);
+            fp_load_chunk<FMT>(rs1, vo, so, l1);
+            x0 = __builtin_amdgcn_raw_buffer_load_b128(rsx, vx, sx, 0);
+            x1 = __builtin_amdgcn_raw_buffer_load_b128(rsx, vx + 16, sx, 0);
+        };
+        auto produce = [&](int s, const FpLoad<FMT>& l0, const FpLoad<FMT>& l1, const u32x4_t& x0, const u32x4_t& x1) {
+            float xv[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xv[i] = __uint_as_float(x0[i]);
+                xv[4 + i] = __uint_as_float(x1[i]);
+            }
+            float v0[8], v1[8];
+            fp_decode<FMT>(l0, v0);
+            fp_decode<FMT>(l1, v1);
+            // chunks past the row were read as zero; their products are stored but never added
+            float* o = out0 + (s & 1) * (kFpRows * 8 * kFpPad);
+#pragma unroll
+            for (int L = 0; L < 8; ++L) {
+                o[L * kFpPad] = mul_rn(v0[L], xv[L]);
+                o[(8 + L) * kFpPad] = mul_rn(v1[L], xv[L]);
+            }
+            lds_barrier();
+        };
+        // round s: segment s into buffer s & 1 (the chain wave reads segment s - 1), then a
+        // barrier; nseg + 1 rounds.  Loads run kFpSlots - 1 segments ahead in kFpSlots register
+        // slots (the loads of rounds past the last segment re-read it: the count stays the same).
+#pragma unroll
+        for (int u = 0; u < kFpSlots - 1; ++u) issue(min(u, nseg - 1), w0[u], w1[u], xa[u], xb[u]);
+        for (int s0 = 0;; s0 += kFpSlots) {  // exits only through the break: the back-edge is steady state
+            bool done = false;
+#pragma unroll
+            for (int u = 0; u < kFpSlots; ++u) {
+                const int sl = (u + kFpSlots - 1) % kFpSlots;
+                issue(min(s0 + u + kFpSlots - 1, nseg - 1), w0[sl], w1[sl], xa[sl], xb[sl]);
+                produce(s0 + u, w0[u], w1[u], xa[u], xb[u]);
+                if (s0 + u + 1 >= nseg) {
+                    done = true;
+                    break;
+                }
+            }
+            if (done) break;
+        }
+        lds_barrier();  // round nseg: the chain wave adds the last segment
+        return;
+    }
+
+    // the chain wave: lane = 8 * row + L
+    const int lane = t - kFpProducers;
+    const int rr = lane >> 3, L = lane & 7;
+    float acc = 0.0f;
+    lds_barrier();  // round 0
+    for (int s = 0; s < nseg; ++s) {
+        const float4* pr = reinterpret_cast<const float4*>(&P[s & 1][lane * kFpPad]);
+        const int n = min(kFpSeg, nch - s * kFpSeg);
+#pragma unroll
+        for (int i = 0; i < kFpSeg / 4; ++i) {
+            const float4 v = pr[i];
+            if (4 * i + 0 < n) acc = add_rn(acc, v.x);
+            if (4 * i + 1 < n) acc = add_rn(acc, v.y);
+            if (4 * i + 2 < n) acc = add_rn(acc, v.z);
+            if (4 * i + 3 < n) acc = add_rn(acc, v.w);
+        }
+        lds_barrier();  // round s + 1
+    }
+    // HSum in lane order over the row's 8 lanes
+    const int base = lane & ~7;
+    float sum = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(acc, base + l, 64));
+    const long long row = r0 + rr;
+    if constexpr (FMT == QR_FMT_F16) {
+        if (!isfinite(sum) && row < a.rows) {
+            // exact decode of the row's lane chain (HalfBitsToFloat, DotKernels.cs:86-100)
+            const uint8_t* w = a.w + row * a.row_bytes;
+            float e = 0.0f;
+            for (int c = 0; c < nch; ++c) {
+                const int k = 8 * c + L;
+                e = add_rn(e, mul_rn(f16_dot_decode(*reinterpret_cast<const uint16_t*>(w + 2 * k)), x[k]));
+            }
+            sum = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(e, base + l, 64));
+        }
+    }
+    if (L == 0 && row < a.rows) a.y[static_cast<long long>(q) * a.rows + row] = sum;
+}
+
+// Single-wave form of the same order: a workgroup is one wave and R <= 8 rows, lane 8r + L
+// the chain (row r, lane L).  The wave streams its rows in segments of 1 KiB per row through a
+// ring of kFwSlots LDS slots filled by direct-to-LDS buffer loads (kFwSlots - 1 segments in
+// flight; completion awaited with explicit vmcnt waits), and each lane walks its chain over
+// the chunks of a segment: weight, x, product, add.  No barrier, no register prefetch.
+constexpr int kFwSlots = 3;
+constexpr int kFwRowPad = 1024 + 16;  // LDS bytes per row segment: rows land on distinct banks
+
+template <int FMT, int R>
+struct FwGeom {
+    static constexpr int B = FMT == QR_FMT_F32 ? 32 : 16;     // bytes per chunk of 8 weights
+    static constexpr int SEG = 1024 / B;                       // chunks per segment
+    static constexpr int XBYTES = SEG * 32;                    // x bytes per segment
+    static constexpr int XDMA = XBYTES / 1024;                 // DMAs of x per segment
+    static constexpr int SLOT = R * kFwRowPad + XBYTES;        // bytes per slot
+    static constexpr int DMAS = R + XDMA;                      // DMAs per segment
+};
+
+template <int FMT>
+__device__ __forceinline__ float fw_weight(const char* p) {
+    if constexpr (FMT == QR_FMT_F32) return *reinterpret_cast<const float*>(p);
+    else if constexpr (FMT == QR_FMT_BF16) return __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p)) << 16);
+    else return f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+}
+
+template <int FMT, int R>
+__global__ __launch_bounds__(64) void matvec_fp_wave(MatVecArgs a) {
+    using Gm = FwGeom<FMT, R>;
+    __shared__ __align__(16) char ring[kFwSlots][Gm::SLOT];
+    const int lane = threadIdx.x;
+    const int rr = lane >> 3, L = lane & 7;
+    const long long r0 = static_cast<long long>(blockIdx.x) * R;
+    const int q = blockIdx.y;
+    const float* x = a.x + static_cast<long long>(q) * a.cols;
+    const int nch = a.cols / 8;
+    const int nseg = (nch + Gm::SEG - 1) / Gm::SEG;
+    const int rbytes = nch * Gm::B;
+
+    __amdgpu_buffer_rsrc_t rs[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {  // rows past the matrix: an empty resource, read as zeros
+        const bool in = r0 + r < a.rows;
+        rs[r] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w + (in ? (r0 + r) * a.row_bytes : 0)),
+                                                  static_cast<short>(0), in ? rbytes : 0, kBufferFlags);
+    }
+    const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), static_cast<short>(0),
+                                                                        nch * 32, kBufferFlags);
+    // segment s into slot s % kFwSlots; past the last segment the last one is read again, so
+    // that every round issues the same number of DMAs
+    auto issue = [&](int s) {
+        s = min(s, nseg - 1);
+        char* slot = ring[s % kFwSlots];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            buffer_load_lds16(rs[r], slot + r * kFwRowPad, static_cast<uint32_t>(16 * lane),
+                              static_cast<uint32_t>(s * 1024));
+#pragma unroll
+        for (int i = 0; i < Gm::XDMA; ++i)
+            buffer_load_lds16(rsx, slot + R * kFwRowPad + 1024 * i, static_cast<uint32_t>(16 * lane),
+                              static_cast<uint32_t>(s * Gm::XBYTES + 1024 * i));
+    };
+
+    float acc = 0.0f;
+    const int wofs = rr * kFwRowPad + (FMT == QR_FMT_F32 ? 4 : 2) * L;
+    const int xofs = R * kFwRowPad + 4 * L;
+#pragma unroll
+    for (int s = 0; s < kFwSlots - 1; ++s) issue(s);
+    for (int s = 0; s < nseg; ++s) {
+        // the slot refilled now was consumed in the previous round (this wave's own reads)
+        issue(s + kFwSlots - 1);
+        wait_vmcnt<(kFwSlots - 1) * Gm::DMAS>();  // segment s has landed
+        asm volatile("" ::: "memory");
+        const char* slot = ring[s % kFwSlots];
+        const int n = min(Gm::SEG, nch - s * Gm::SEG);
+        if (n == Gm::SEG) {
+#pragma unroll 16
+            for (int c = 0; c < Gm::SEG; ++c)
+                acc = add_rn(acc, mul_rn(fw_weight<FMT>(slot + wofs + c * Gm::B),
+                                         *reinterpret_cast<const float*>(slot + xofs + c * 32)));
+        } else {
+            for (int c = 0; c < n; ++c)
+                acc = add_rn(acc, mul_rn(fw_weight<FMT>(slot + wofs + c * Gm::B),
+                                         *reinterpret_cast<const float*>(slot + xofs + c * 32)));
+        }
+        asm volatile("" ::: "memory");  // this slot's reads stay before its refill
+    }
+    wait_dma();
+    // HSum in lane order over the row's 8 lanes
+    const int base = lane & ~7;
+    float sum = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(acc, base + l, 64));
+    const long long row = r0 + rr;
+    if constexpr (FMT == QR_FMT_F16) {
+        if (!isfinite(sum) && rr < R && row < a.rows) {
+            // exact decode of the row's lane chain (HalfBitsToFloat, DotKernels.cs:86-100)
+            const uint8_t* w = a.w + row * a.row_bytes;
+            float e = 0.0f;
+            for (int c = 0; c < nch; ++c) {
+                const int k = 8 * c + L;
+                e = add_rn(e, mul_rn(f16_dot_decode(*reinterpret_cast<const uint16_t*>(w + 2 * k)), x[k]));
+            }
+            sum = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(e, base + l, 64));
+        }
+    }
+    if (L == 0 && rr < R && row < a.rows) a.y[static_cast<long long>(q) * a.rows + row] = sum;
+}
+
 // fp weight k of a staged row
 template <int FMT>
 __device__ __forceinline__ float fp_weight(const uint8_t* row, int k) {
@@ -970,12 +1254,31 @@ bool matvec_shape_ok(int fmt, int cols) {
     return !fp || cols % 8 == 0;
 }
 
+// The producer/consumer fp form needs 16-byte aligned rows and x.
+template <int FMT>
+hipError_t launch_fp(const MatVecArgs& a, hipStream_t stream) {
+    if (reinterpret_cast<uintptr_t>(a.w) % 16 || a.row_bytes % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
+        a.cols % 8)
+        return launch_fmt<FMT>(a, stream);
+#ifndef QR_MV_FP_FORM
+#define QR_MV_FP_FORM 1
+#endif
+    if (QR_MV_FP_FORM == 1) {
+        const dim3 grid(static_cast<unsigned>((a.rows + 7) / 8), static_cast<unsigned>(a.nq));
+        hipLaunchKernelGGL((matvec_fp_wave<FMT, 8>), grid, dim3(64), 0, stream, a);
+        return hipGetLastError();
+    }
+    const dim3 grid(static_cast<unsigned>((a.rows + kFpRows - 1) / kFpRows), static_cast<unsigned>(a.nq));
+    hipLaunchKernelGGL(matvec_fp_kernel<FMT>, grid, dim3(kFpThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
     if (a.nq == 0 || a.rows == 0) return hipSuccess;
     switch (a.fmt) {
-    case QR_FMT_F32: return launch_fmt<QR_FMT_F32>(a, stream);
-    case QR_FMT_F16: return launch_fmt<QR_FMT_F16>(a, stream);
-    case QR_FMT_BF16: return launch_fmt<QR_FMT_BF16>(a, stream);
+    case QR_FMT_F32: return launch_fp<QR_FMT_F32>(a, stream);
+    case QR_FMT_F16: return launch_fp<QR_FMT_F16>(a, stream);
+    case QR_FMT_BF16: return launch_fp<QR_FMT_BF16>(a, stream);
     case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
     case QR_FMT_Q8_0: return launch_fmt<QR_FMT_Q8_0>(a, stream);
     case QR_FMT_Q4_K: {
