@@ -388,24 +388,116 @@ __global__ __launch_bounds__(kMvThreads) void matvec_q4k_kernel(MatVecArgs a, Mv
     }
 }
 
-// Persistent form: workgroup w takes row tiles w, w + G, w + 2G, ... (G = gridDim.x, R rows a
-// tile).  x and its sub-block sums stay in registers for all of them, the next tile's weights
-// are loaded while the current tile is computed (two register buffers, the loop unrolled by
-// two so that each half waits only for its own loads), every tile's terms stay in LDS, and the
-// in-order sums of all the workgroup's rows run at the end.  blockDim = rg * tpg threads.
-struct MvQ4kP {
+// Persistent form of the block formats: workgroup w takes row tiles w, w + G, w + 2G, ...
+// (G = gridDim.x, R rows a tile).  Thread (row group g, item column pc) owns one item of every
+// row (Q4_K: a sub-block pair, 64 columns, two terms; Q8_0: a block pair, 64 columns, two
+// terms): its x values stay in registers for all tiles, the next tile's weights are loaded
+// while the current tile is computed (two register buffers, the loop unrolled by two so that
+// each half waits only for its own loads), every tile's terms stay in LDS, and the in-order
+// sums of all the workgroup's rows run at the end.  blockDim = rg * tpg threads.
+struct MvBlkP {
     int P, tpg, rg, R, tstride;
     int ntiles;   // ceil(rows / R)
 };
 
+// Q4_K (DotKernels.cs:322-373): item pc = 4*block + j; loads: the block header and the two
+// 16-byte quant vectors of pair j.
+struct PolQ4K {
+    static constexpr int kLoads = 3;
+    static constexpr int kWords = 4;  // dwords per load
+    struct Lane {
+        int j;
+        float ss0, ss1;
+        float xv[64];
+    };
+    __device__ static void offsets(int pc, uint32_t (&o)[kLoads]) {
+        const uint32_t b = static_cast<uint32_t>((pc >> 2) * 144);
+        o[0] = b;
+        o[1] = b + 16 + 32 * (pc & 3);
+        o[2] = o[1] + 16;
+    }
+    __device__ static void prep(Lane& l, const float* x, int pc) {
+        l.j = pc & 3;
+        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 f = x4[i];
+            l.xv[4 * i] = f.x;
+            l.xv[4 * i + 1] = f.y;
+            l.xv[4 * i + 2] = f.z;
+            l.xv[4 * i + 3] = f.w;
+        }
+        l.ss0 = 0.0f;  // SubSum over the 32 values of each sub-block, in order
+        l.ss1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) l.ss0 = add_rn(l.ss0, l.xv[i]);
+#pragma unroll
+        for (int i = 32; i < 64; ++i) l.ss1 = add_rn(l.ss1, l.xv[i]);
+    }
+    __device__ static void terms(const Lane& l, const u32x4_t (&v)[kLoads], float& t0, float& t1) {
+        q4k_pair_terms(v[0], v[1], v[2], l.j, l.xv, l.ss0, l.ss1, t0, t1);
+    }
+};
+
+// Q8_0 (DotKernels.cs:183-230): item pc = block pair (blocks 2pc, 2pc+1: 68 bytes, 4-byte
+// aligned when the row is); loads: the 17 dwords of the pair.  Per block: lane L sums
+// q[L]x[L], q[8+L]x[8+L], q[16+L]x[16+L], q[24+L]x[24+L] in order, HSum, times d.
+struct PolQ8 {
+    static constexpr int kLoads = 17;
+    static constexpr int kWords = 1;
+    struct Lane {
+        float xv[64];
+    };
+    __device__ static void offsets(int pc, uint32_t (&o)[kLoads]) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) o[i] = static_cast<uint32_t>(68 * pc + 4 * i);
+    }
+    __device__ static void prep(Lane& l, const float* x, int pc) {
+        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 f = x4[i];
+            l.xv[4 * i] = f.x;
+            l.xv[4 * i + 1] = f.y;
+            l.xv[4 * i + 2] = f.z;
+            l.xv[4 * i + 3] = f.w;
+        }
+    }
+    // byte k of the pair
+    __device__ static int sbyte(const uint32_t (&w)[kLoads], int k) {
+        return static_cast<int8_t>((w[k >> 2] >> (8 * (k & 3))) & 0xFFu);
+    }
+    __device__ static float block(const uint32_t (&w)[kLoads], int b0, const float* x) {
+        const uint32_t hb = (w[b0 >> 2] >> (8 * (b0 & 3))) & 0xFFFFu;  // b0 even: one dword
+        const float d = f16_bits_to_f32(static_cast<uint16_t>(hb));
+        float acc[8];
+#pragma unroll
+        for (int L = 0; L < 8; ++L) {
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                a = add_rn(a, mul_rn(static_cast<float>(sbyte(w, b0 + 2 + 8 * k + L)), x[8 * k + L]));
+            acc[L] = a;
+        }
+        return mul_rn(d, hsum8(acc));
+    }
+    __device__ static void terms(const Lane& l, const uint32_t (&v)[kLoads], float& t0, float& t1) {
+        t0 = block(v, 0, l.xv);
+        t1 = block(v, 34, l.xv + 32);
+    }
+};
+
+template <class Pol> struct PolLoad { typedef u32x4_t type; };
+template <> struct PolLoad<PolQ8> { typedef uint32_t type; };
+
 // Loads of one tile through a buffer resource made for it (uniform base and size), so that a
-// tile costs scalar arithmetic only: lane offsets vh/vq (block header, first quant vector of
-// the lane's pair, per row) are fixed for the whole kernel.  Rows past the end of the matrix
-// lie outside the resource and read as zero; their terms are never summed.
-template <int RPT>
-__device__ __forceinline__ void q4k_load(const MatVecArgs& a, const MvQ4kP& k, int tile, const uint32_t (&vh)[RPT],
-                                         const uint32_t (&vq)[RPT], u32x4_t (&h)[RPT], u32x4_t (&qa)[RPT],
-                                         u32x4_t (&qb)[RPT]) {
+// tile costs scalar arithmetic only: the lane offsets (per row) are fixed for the whole kernel.
+// Rows past the end of the matrix lie outside the resource and read as zero; their terms are
+// never summed.
+template <class Pol, int RPT>
+__device__ __forceinline__ void blk_load(const MatVecArgs& a, const MvBlkP& k, int tile,
+                                         const uint32_t (&off)[RPT][Pol::kLoads],
+                                         typename PolLoad<Pol>::type (&v)[RPT][Pol::kLoads]) {
     // 32-bit uniform arithmetic (rows < 2^31 and R * row_bytes < 2^31 are checked on the host):
     // a 64-bit compare would be done in vector registers
     const int r0 = tile * k.R;
@@ -414,60 +506,49 @@ __device__ __forceinline__ void q4k_load(const MatVecArgs& a, const MvQ4kP& k, i
         const_cast<uint8_t*>(a.w + static_cast<long long>(r0) * a.row_bytes), static_cast<short>(0), nrec,
         kBufferFlags);
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        h[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vh[r], 0, 0);
-        qa[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vq[r], 0, 0);
-        qb[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, vq[r] + 16, 0, 0);
-    }
+    for (int r = 0; r < RPT; ++r)
+#pragma unroll
+        for (int i = 0; i < Pol::kLoads; ++i) {
+            if constexpr (Pol::kWords == 4) v[r][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[r][i], 0, 0);
+            else v[r][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, off[r][i], 0, 0);
+        }
 }
 
-template <int RPT>
-__global__ __launch_bounds__(512) void matvec_q4k_persistent(MatVecArgs a, MvQ4kP k) {
+template <class Pol, int RPT>
+__global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlkP k) {
+    typedef typename PolLoad<Pol>::type V;
     extern __shared__ __align__(16) uint8_t mv_lds[];
     float* terms = reinterpret_cast<float*>(mv_lds);
     const int t = threadIdx.x;
     const int g = t / k.tpg;
     const bool active = t - g * k.tpg < k.P;
-    // lanes past the row's pairs load and compute pair P-1 and store nothing: no branch
+    // lanes past the row's items load and compute item P-1 and store nothing: no branch
     // around the loads, so the wait counts stay exact
     const int pc = min(t - g * k.tpg, k.P - 1);
-    const int blk = pc >> 2, j = pc & 3;
     const int G = gridDim.x;
     const int q = blockIdx.y;
     const float* x = a.x + static_cast<long long>(q) * a.cols;
     const int last = k.ntiles - 1;
 
-    uint32_t vh[RPT], vq[RPT];
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        vh[r] = static_cast<uint32_t>((g * RPT + r) * a.row_bytes + blk * 144);
-        vq[r] = vh[r] + 16 + 32 * j;
-    }
-    u32x4_t hA[RPT], qaA[RPT], qbA[RPT], hB[RPT], qaB[RPT], qbB[RPT];
-    int it = blockIdx.x;
-    q4k_load<RPT>(a, k, it, vh, vq, hA, qaA, qbA);
-    float xv[64];
-    float ss0 = 0.0f, ss1 = 0.0f;
+    uint32_t off[RPT][Pol::kLoads];
     {
-        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+        uint32_t o[Pol::kLoads];
+        Pol::offsets(pc, o);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float4 f = x4[i];
-            xv[4 * i] = f.x;
-            xv[4 * i + 1] = f.y;
-            xv[4 * i + 2] = f.z;
-            xv[4 * i + 3] = f.w;
-        }
+        for (int r = 0; r < RPT; ++r)
 #pragma unroll
-        for (int i = 0; i < 32; ++i) ss0 = add_rn(ss0, xv[i]);
-#pragma unroll
-        for (int i = 32; i < 64; ++i) ss1 = add_rn(ss1, xv[i]);
+            for (int i = 0; i < Pol::kLoads; ++i) off[r][i] = static_cast<uint32_t>((g * RPT + r) * a.row_bytes) + o[i];
     }
-    auto compute = [&](const u32x4_t (&h)[RPT], const u32x4_t (&qa)[RPT], const u32x4_t (&qb)[RPT], int slot) {
+    V vA[RPT][Pol::kLoads], vB[RPT][Pol::kLoads];
+    int it = blockIdx.x;
+    blk_load<Pol, RPT>(a, k, it, off, vA);
+    typename Pol::Lane lane;
+    Pol::prep(lane, x, pc);
+    auto compute = [&](const V (&v)[RPT][Pol::kLoads], int slot) {
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
             float t0, t1;
-            q4k_pair_terms(h[r], qa[r], qb[r], j, xv, ss0, ss1, t0, t1);
+            Pol::terms(lane, v[r], t0, t1);
             if (active)
                 *reinterpret_cast<float2*>(terms + ((slot * k.R) + g * RPT + r) * k.tstride + 2 * pc) =
                     make_float2(t0, t1);
@@ -476,13 +557,13 @@ __global__ __launch_bounds__(512) void matvec_q4k_persistent(MatVecArgs a, MvQ4k
     int slot = 0;
     for (;;) {  // exits only through the breaks: the back-edge is the steady state
         const int n1 = it + G;
-        q4k_load<RPT>(a, k, min(n1, last), vh, vq, hB, qaB, qbB);
-        compute(hA, qaA, qbA, slot++);
+        blk_load<Pol, RPT>(a, k, min(n1, last), off, vB);
+        compute(vA, slot++);
         if (n1 > last) break;
         it = n1;
         const int n2 = it + G;
-        q4k_load<RPT>(a, k, min(n2, last), vh, vq, hA, qaA, qbA);
-        compute(hB, qaB, qbB, slot++);
+        blk_load<Pol, RPT>(a, k, min(n2, last), off, vA);
+        compute(vB, slot++);
         if (n2 > last) break;
         it = n2;
     }
@@ -704,11 +785,16 @@ struct FwGeom {
     static constexpr int DMAS = R + XDMA;                      // DMAs per segment
 };
 
+// The product of the weight at p (LDS) and x.  F16: fma(w, x, +0) in one v_fma_mix_f32 (the
+// half converted exactly inside); it equals the rounded product w*x except that a -0 product
+// becomes +0, which no chain can tell apart: a lane sum starts at +0 and never becomes -0
+// (x + y is -0 only for two -0 operands), and for any other value v + (-0) = v + (+0).
 template <int FMT>
-__device__ __forceinline__ float fw_weight(const char* p) {
-    if constexpr (FMT == QR_FMT_F32) return *reinterpret_cast<const float*>(p);
-    else if constexpr (FMT == QR_FMT_BF16) return __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p)) << 16);
-    else return f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+__device__ __forceinline__ float fw_product(const char* p, float x) {
+    if constexpr (FMT == QR_FMT_F32) return mul_rn(*reinterpret_cast<const float*>(p), x);
+    else if constexpr (FMT == QR_FMT_BF16)
+        return mul_rn(__uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(p)) << 16), x);
+    else return __builtin_fmaf(static_cast<float>(*reinterpret_cast<const _Float16*>(p)), x, 0.0f);
 }
 
 template <int FMT, int R>
@@ -763,12 +849,12 @@ __global__ __launch_bounds__(64) void matvec_fp_wave(MatVecArgs a) {
         if (n == Gm::SEG) {
 #pragma unroll 16
             for (int c = 0; c < Gm::SEG; ++c)
-                acc = add_rn(acc, mul_rn(fw_weight<FMT>(slot + wofs + c * Gm::B),
-                                         *reinterpret_cast<const float*>(slot + xofs + c * 32)));
+                acc = add_rn(acc, fw_product<FMT>(slot + wofs + c * Gm::B,
+                                                  *reinterpret_cast<const float*>(slot + xofs + c * 32)));
         } else {
             for (int c = 0; c < n; ++c)
-                acc = add_rn(acc, mul_rn(fw_weight<FMT>(slot + wofs + c * Gm::B),
-                                         *reinterpret_cast<const float*>(slot + xofs + c * 32)));
+                acc = add_rn(acc, fw_product<FMT>(slot + wofs + c * Gm::B,
+                                                  *reinterpret_cast<const float*>(slot + xofs + c * 32)));
         }
         asm volatile("" ::: "memory");  // this slot's reads stay before its refill
     }
@@ -1183,37 +1269,41 @@ bool q4k_config(const MatVecArgs& a, MvQ4k* k, int* rpt_out) {
     return static_cast<size_t>(k->R) * k->tstride * 4 <= 64 * 1024;
 }
 
-#ifndef QR_MV_Q4KP_RPT
-#define QR_MV_Q4KP_RPT 2
+#ifndef QR_MV_BLKP_RPT
+#define QR_MV_BLKP_RPT 2
 #endif
-#ifndef QR_MV_Q4KP_WGCU
-#define QR_MV_Q4KP_WGCU 3
+#ifndef QR_MV_BLKP_WGCU
+#define QR_MV_BLKP_WGCU 3
 #endif
 
-// The persistent Q4_K form for rows of at most 512 pairs (32768 columns): false when the
-// terms of a workgroup's tiles would not fit in 64 KiB of LDS.
-bool q4k_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
-    if (a.fmt != QR_FMT_Q4_K || reinterpret_cast<uintptr_t>(a.w) % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
-        a.row_bytes % 16)
-        return false;
-    MvQ4kP k{};
+// The persistent form for Q4_K (64-column items: rows of at most 512 items, 32768 columns) and
+// Q8_0 (block pairs: whole pairs and 4-byte aligned rows): false when the shape does not fit or
+// the terms of a workgroup's tiles would not fit in 64 KiB of LDS.
+bool blk_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
+    const bool q4k = a.fmt == QR_FMT_Q4_K, q8 = a.fmt == QR_FMT_Q8_0;
+    if (!(q4k || q8) || reinterpret_cast<uintptr_t>(a.x) % 16 || a.cols % 64) return false;
+    if (q4k && (reinterpret_cast<uintptr_t>(a.w) % 16 || a.row_bytes % 16)) return false;
+    if (q8 && (reinterpret_cast<uintptr_t>(a.w) % 4 || a.row_bytes % 4)) return false;
+    MvBlkP k{};
     k.P = a.cols / 64;
     if (k.P > 512) return false;
     k.tpg = (k.P + 63) / 64 * 64;
     k.rg = std::max(1, kMvThreads / k.tpg);
-    constexpr int rpt = QR_MV_Q4KP_RPT;
+    // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts
+    const int rpt = q4k ? QR_MV_BLKP_RPT : 1;
     k.R = k.rg * rpt;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
     k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
     if (static_cast<long long>(k.R) * a.row_bytes >= (1LL << 31) || a.rows >= (1LL << 31) - k.R) return false;
     const int threads = k.rg * k.tpg;
-    const int wg_per_cu = std::max(1, QR_MV_Q4KP_WGCU * 256 / threads);
+    const int wg_per_cu = std::max(1, QR_MV_BLKP_WGCU * 256 / threads);
     int G = std::min(k.ntiles, 256 * wg_per_cu);
     const int tpw = (k.ntiles + G - 1) / G;
     const size_t lds = static_cast<size_t>(tpw) * k.R * k.tstride * 4;
     if (lds > 64 * 1024) return false;
     const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
-    hipLaunchKernelGGL(matvec_q4k_persistent<rpt>, grid, dim3(threads), lds, stream, a, k);
+    if (q4k) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, QR_MV_BLKP_RPT>), grid, dim3(threads), lds, stream, a, k);
+    else hipLaunchKernelGGL((matvec_blk_persistent<PolQ8, 1>), grid, dim3(threads), lds, stream, a, k);
     *err = hipGetLastError();
     return true;
 }
@@ -1280,10 +1370,14 @@ hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
     case QR_FMT_F16: return launch_fp<QR_FMT_F16>(a, stream);
     case QR_FMT_BF16: return launch_fp<QR_FMT_BF16>(a, stream);
     case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
-    case QR_FMT_Q8_0: return launch_fmt<QR_FMT_Q8_0>(a, stream);
+    case QR_FMT_Q8_0: {
+        hipError_t e;
+        if (blk_persistent_launch(a, stream, &e)) return e;
+        return launch_fmt<QR_FMT_Q8_0>(a, stream);
+    }
     case QR_FMT_Q4_K: {
         hipError_t e;
-        if (q4k_persistent_launch(a, stream, &e)) return e;
+        if (blk_persistent_launch(a, stream, &e)) return e;
         MvQ4k k;
         int rpt;
         if (q4k_config(a, &k, &rpt)) return launch_q4k(a, k, rpt, stream);
