@@ -111,6 +111,74 @@ __device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g,
     for (int e = 0; e < 4; ++e) base[g.offset(phys, plane, kvh, slot, d + e)] = b[e];
 }
 
+// Same work with the loads of all of a thread's items issued before the cos/sin of the
+// position are computed: the libm calls overlap the memory latency instead of preceding it.
+// IPT = items per thread (heads * head_dim / 8 <= 256 * IPT).
+template <int IPT>
+__global__ void __launch_bounds__(256) rope_append_items_kernel(const RopeAppendArgs a) {
+    const AppendArgs& g = a.app;
+    const int D = g.geom.head_dim;
+    const int half = D >> 1;
+    const int kv_heads = g.geom.kv_heads;
+    const int q_heads = a.q ? a.q_width / D : 0;
+    const int heads = kv_heads + q_heads;
+    const int per_head = half / 4;
+    const int nitems = heads * per_head;
+    const long long row = blockIdx.x;  // one position per workgroup
+    float4 x0[IPT], x1[IPT], w0[IPT], w1[IPT];
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+        const int it = min(static_cast<int>(threadIdx.x) + 256 * k, nitems - 1);  // past the end: a valid item, not stored
+        const int h = it / per_head;
+        const int d = 4 * (it - h * per_head);
+        const float* src = h < kv_heads ? static_cast<const float*>(g.src[0]) + row * g.src_stride + h * D
+                                        : a.q + row * a.q_width + (h - kv_heads) * D;
+        x0[k] = *reinterpret_cast<const float4*>(src + d);
+        x1[k] = *reinterpret_cast<const float4*>(src + d + half);
+        const float* v = static_cast<const float*>(g.src[1]) + row * g.src_stride + min(h, kv_heads - 1) * D;
+        w0[k] = *reinterpret_cast<const float4*>(v + d);
+        w1[k] = *reinterpret_cast<const float4*>(v + d + half);
+    }
+    __shared__ float cs[2][kMaxRopeHalf];
+    for (int i = threadIdx.x; i < half; i += 256) {
+        const float ang = mul_rn(static_cast<float>(g.pos0 + row), a.freq[i]);
+        cs[0][i] = cosf(ang);
+        cs[1][i] = sinf(ang);
+    }
+    __syncthreads();
+    const int t = g.pos0 + static_cast<int>(row);
+    const long long phys = g.page_table[t >> kPageShift];
+    const int slot = t & (kPageTokens - 1);
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+        const int it = threadIdx.x + 256 * k;
+        if (it >= nitems) break;
+        const int h = it / per_head;
+        const int d = 4 * (it - h * per_head);
+        const float4 c = *reinterpret_cast<const float4*>(&cs[0][d]);
+        const float4 sn = *reinterpret_cast<const float4*>(&cs[1][d]);
+        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
+        const float a0[4] = {x0[k].x, x0[k].y, x0[k].z, x0[k].w}, a1[4] = {x1[k].x, x1[k].y, x1[k].z, x1[k].w};
+        float y0[4], y1[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            y0[e] = sub_rn(mul_rn(a0[e], cc[e]), mul_rn(a1[e], ss[e]));
+            y1[e] = add_rn(mul_rn(a0[e], ss[e]), mul_rn(a1[e], cc[e]));
+        }
+        if (h < kv_heads) {
+            store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d, y0);
+            store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d + half, y1);
+            const float v0[4] = {w0[k].x, w0[k].y, w0[k].z, w0[k].w}, v1[4] = {w1[k].x, w1[k].y, w1[k].z, w1[k].w};
+            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d, v0);
+            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d + half, v1);
+        } else {
+            float* q = a.q + row * a.q_width + (h - kv_heads) * D;
+            *reinterpret_cast<float4*>(q + d) = make_float4(y0[0], y0[1], y0[2], y0[3]);
+            *reinterpret_cast<float4*>(q + d + half) = make_float4(y1[0], y1[1], y1[2], y1[3]);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) rope_append_kernel(const RopeAppendArgs a) {
     const AppendArgs& g = a.app;
     const int D = g.geom.head_dim;
@@ -199,7 +267,20 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_append_kernel, dim3((a.app.n + kRopeRows - 1) / kRopeRows), dim3(256), 0, stream, a);
+    const int D = a.app.geom.head_dim;
+    const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
+    const int ipt = (heads * (D / 8) + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(a.app.n));
+    switch (ipt) {
+    case 1: hipLaunchKernelGGL(rope_append_items_kernel<1>, grid, dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(rope_append_items_kernel<2>, grid, dim3(256), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL(rope_append_items_kernel<3>, grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(rope_append_items_kernel<4>, grid, dim3(256), 0, stream, a); break;
+    case 5: case 6: hipLaunchKernelGGL(rope_append_items_kernel<6>, grid, dim3(256), 0, stream, a); break;
+    case 7: case 8: hipLaunchKernelGGL(rope_append_items_kernel<8>, grid, dim3(256), 0, stream, a); break;
+    default:
+        hipLaunchKernelGGL(rope_append_kernel, dim3((a.app.n + kRopeRows - 1) / kRopeRows), dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
