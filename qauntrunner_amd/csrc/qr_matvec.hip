@@ -11,11 +11,14 @@
 //   Q6_K          per block: 256 products summed in (half, l, q1..q4) order; sum += d*dot
 // Every product and sum is separately rounded (mul_rn / add_rn / sub_rn).
 //
-// A workgroup takes R rows and walks the columns in slabs: it stages the slab of its rows
-// and the slab of x in LDS (all loads issued before any store), computes the block terms
-// of every (row, block) in parallel, and one thread per row adds them in order.  The
-// F32/F16/BF16 lane sums are the 8R threads (row, lane), each walking its lane in order.
-// HBM-bound: every weight byte is read once per input vector.
+// Kernels (every weight byte is read once per input vector):
+//   matvec_blk_persistent  Q4_K: x in registers per 64-column item, row tiles double
+//                          buffered in registers, block terms per thread, in-order sums last
+//   matvec_blk_ring        Q8_0: the same items with row tiles streamed through an LDS ring
+//   matvec_fp_wave         F32/F16/BF16: one wave per 8 rows, lane = (row, DotF32 lane),
+//                          1 KiB row segments through an LDS ring
+//   matvec_kernel          everything else (Q4_0, Q6_K, unaligned rows): LDS tiles of R rows,
+//                          block terms in parallel, one thread per row adds them in order
 #include <algorithm>
 
 #include "qr_matvec.hpp"
@@ -311,83 +314,6 @@ __device__ __forceinline__ void q4k_pair_terms(const u32x4_t h, const u32x4_t qa
     }
 }
 
-// Thread (row group g, pair column pc) computes the two terms of RPT rows of pair pc; the
-// terms go to LDS and one thread per row then adds them in order.  Weight loads of all RPT
-// rows and the 64 x values are issued before any arithmetic.
-struct MvQ4k {
-    int P;        // pairs per row (cols / 64)
-    int tpg;      // threads per row group (a multiple of 64, <= 256)
-    int rg;       // row groups per workgroup
-    int R;        // rows per workgroup (rg * RPT)
-    int tstride;  // floats per LDS term row (2P rounded up to 4, plus 4)
-};
-
-template <int RPT>
-__global__ __launch_bounds__(kMvThreads) void matvec_q4k_kernel(MatVecArgs a, MvQ4k k) {
-    extern __shared__ __align__(16) uint8_t mv_lds[];
-    float* terms = reinterpret_cast<float*>(mv_lds);
-    const int t = threadIdx.x;
-    const int g = t / k.tpg;
-    const long long r0 = static_cast<long long>(blockIdx.x) * k.R;
-    const int q = blockIdx.y;
-    const float* x = a.x + static_cast<long long>(q) * a.cols;
-    if (g < k.rg) {
-        for (int pc = t - g * k.tpg; pc < k.P; pc += k.tpg) {
-            const int blk = pc >> 2, j = pc & 3;
-            u32x4_t h[RPT], qa[RPT], qb[RPT];
-#pragma unroll
-            for (int r = 0; r < RPT; ++r) {
-                const long long row = min(r0 + g * RPT + r, a.rows - 1);
-                const uint8_t* p = a.w + row * a.row_bytes + blk * 144;
-                h[r] = *reinterpret_cast<const u32x4_t*>(p);
-                qa[r] = *reinterpret_cast<const u32x4_t*>(p + 16 + 32 * j);
-                qb[r] = *reinterpret_cast<const u32x4_t*>(p + 32 + 32 * j);
-            }
-            float xv[64];
-            const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float4 f = x4[i];
-                xv[4 * i] = f.x;
-                xv[4 * i + 1] = f.y;
-                xv[4 * i + 2] = f.z;
-                xv[4 * i + 3] = f.w;
-            }
-            float ss0 = 0.0f, ss1 = 0.0f;  // SubSum over the 32 values of each sub-block, in order
-#pragma unroll
-            for (int i = 0; i < 32; ++i) ss0 = add_rn(ss0, xv[i]);
-#pragma unroll
-            for (int i = 32; i < 64; ++i) ss1 = add_rn(ss1, xv[i]);
-#pragma unroll
-            for (int r = 0; r < RPT; ++r) {
-                float t0, t1;
-                q4k_pair_terms(h[r], qa[r], qb[r], j, xv, ss0, ss1, t0, t1);
-                *reinterpret_cast<float2*>(terms + (g * RPT + r) * k.tstride + 2 * pc) = make_float2(t0, t1);
-            }
-        }
-    }
-    __syncthreads();
-    if (t < k.R && r0 + t < a.rows) {  // in order, 16 terms (4 float4 reads) per batch
-        const float4* tr = reinterpret_cast<const float4*>(terms + t * k.tstride);
-        const int nt = 2 * k.P;
-        float sum = 0.0f;
-        for (int i = 0; i < nt; i += 16) {
-            float4 vv[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vv[c] = tr[min(i / 4 + c, (nt - 1) / 4)];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int base = i + 4 * c;
-                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
-                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
-                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
-                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
-            }
-        }
-        a.y[static_cast<long long>(q) * a.rows + r0 + t] = sum;
-    }
-}
-
 // Persistent form of the block formats: workgroup w takes row tiles w, w + G, w + 2G, ...
 // (G = gridDim.x, R rows a tile).  Thread (row group g, item column pc) owns one item of every
 // row (Q4_K: a sub-block pair, 64 columns, two terms; Q8_0: a block pair, 64 columns, two
@@ -593,182 +519,118 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
     }
 }
 
-// ---- F32 / F16 / BF16 (DotF32 order, DotKernels.cs:52-100): producer/consumer workgroups.
-// Row r's lane L accumulates k = 8c + L over the chunks c in order, so every row is 8 serial
-// chains.  A workgroup takes 8 rows.  Four producer waves stream the rows in segments of 64
-// chunks (16-byte loads two segments ahead), form the products w*x and write them to LDS
-// chain-major, P[row][L][c]; the fifth wave holds the 64 chains (row, L) and adds each
-// segment in order while the producers fill the other buffer.  F16 weights are decoded with
-// v_cvt_f32_f16, exact for every half but those with exponent 31, which the reference's vector
-// converter reads as finite 2^16-scale values; such a half makes its product, hence the row,
-// non-finite, and a row whose result is not finite is recomputed with the exact decoder.
-constexpr int kFpRows = 8;
-constexpr int kFpSeg = 64;                      // chunks of 8 columns per segment
-constexpr int kFpPad = kFpSeg + 4;              // floats per (row, lane) product row: distinct banks
-constexpr int kFpProducers = 256;
-constexpr int kFpThreads = kFpProducers + 64;   // + the chain wave
-#ifndef QR_MV_FP_SLOTS
-#define QR_MV_FP_SLOTS 6
-#endif
-constexpr int kFpSlots = QR_MV_FP_SLOTS;         // register slots: loads run kFpSlots - 1 segments ahead
+// Ring form of the block formats: the same items and in-order sums as matvec_blk_persistent,
+// but row tiles stream into an LDS ring of kRingSlots slots by direct-to-LDS buffer loads
+// (kRingSlots - 1 tiles in flight, explicit vmcnt waits), so the prefetch depth costs no
+// registers.  A tile is R rows (R * row_bytes <= 4 KiB * U); wave w loads its 1 KiB units
+// w, w + 4, ... of it.  Per tile: wait for this wave's units, barrier (every wave's units have
+// landed and the slot refilled next has been read), refill, compute the tile's terms from LDS.
+constexpr int kRingSlots = 3;  // deeper rings measured slower: fewer workgroups fit per CU
 
-template <int FMT> struct FpLoad {               // one row's chunk (8 weights)
-    u32x4_t w[FMT == QR_FMT_F32 ? 2 : 1];
+struct MvRing {
+    int P, tpg, rg, R, tstride;
+    int ntiles;
+    int slot_bytes;  // 4096 * U
 };
 
-// chunk cl of segment s of a row (buffer resource rs): lane offset vo = 16 cl (F32: 32 cl),
-// segment offset so uniform; chunks past the row read as zero
-template <int FMT>
-__device__ __forceinline__ void fp_load_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so, FpLoad<FMT>& l) {
-    l.w[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 0);
-    if constexpr (FMT == QR_FMT_F32) l.w[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 16, so, 0);
-}
-
-template <int FMT>
-__device__ __forceinline__ void fp_decode(const FpLoad<FMT>& l, float (&v)[8]) {
-    if constexpr (FMT == QR_FMT_F32) {
+template <class Pol, int RPT>
+__device__ __forceinline__ void ring_read(const char* tile, int row_bytes, int g, int pc,
+                                          typename PolLoad<Pol>::type (&v)[RPT][Pol::kLoads]) {
+    uint32_t o[Pol::kLoads];
+    Pol::offsets(pc, o);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = __uint_as_float(l.w[0][i]);
-            v[4 + i] = __uint_as_float(l.w[1][i]);
-        }
-    } else {
+    for (int r = 0; r < RPT; ++r) {
+        const char* rowp = tile + (g * RPT + r) * row_bytes;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w = l.w[0][i];
-            if constexpr (FMT == QR_FMT_BF16) {
-                v[2 * i] = __uint_as_float(w << 16);
-                v[2 * i + 1] = __uint_as_float(w & 0xFFFF0000u);
-            } else {
-                v[2 * i] = f16_bits_to_f32(static_cast<uint16_t>(w & 0xFFFFu));
-                v[2 * i + 1] = f16_bits_to_f32(static_cast<uint16_t>(w >> 16));
-            }
+        for (int i = 0; i < Pol::kLoads; ++i) {
+            if constexpr (Pol::kWords == 4) v[r][i] = *reinterpret_cast<const u32x4_t*>(rowp + o[i]);
+            else v[r][i] = *reinterpret_cast<const uint32_t*>(rowp + o[i]);
         }
     }
 }
 
-template <int FMT>
-__global__ __launch_bounds__(kFpThreads) void matvec_fp_kernel(MatVecArgs a) {
-    __shared__ __align__(16) float P[2][kFpRows * 8 * kFpPad];
+template <class Pol, int RPT, int U>
+__global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
+    typedef typename PolLoad<Pol>::type V;
+    extern __shared__ __align__(1024) char ring_lds[];
+    float* terms = reinterpret_cast<float*>(ring_lds + kRingSlots * k.slot_bytes);
     const int t = threadIdx.x;
-    const long long r0 = static_cast<long long>(blockIdx.x) * kFpRows;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // four waves
+    const int g = t / k.tpg;
+    const bool active = t - g * k.tpg < k.P;
+    const int pc = min(t - g * k.tpg, k.P - 1);
+    const int G = gridDim.x;
     const int q = blockIdx.y;
     const float* x = a.x + static_cast<long long>(q) * a.cols;
-    const int nch = a.cols / 8;
-    const int nseg = (nch + kFpSeg - 1) / kFpSeg;
+    const int cnt = (k.ntiles - static_cast<int>(blockIdx.x) + G - 1) / G;  // tiles of this workgroup, >= 1
 
-    if (t < kFpProducers) {
-        // chunk cl of every segment, rows 2pr and 2pr+1
-        // Rows 2pr and 2pr+1 are uniform in a wave: each is a buffer resource and a chunk is a
-        // lane offset plus a uniform segment offset, so the loop costs no vector address
-        // arithmetic (rows past the matrix read row rows-1 and are never stored).
-        const int cl = t & (kFpSeg - 1), pr = __builtin_amdgcn_readfirstlane(t >> 6);
-        constexpr int B = FMT == QR_FMT_F32 ? 32 : 16;
-        const int rbytes = nch * B;
-        const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(a.w + min(r0 + 2 * pr, a.rows - 1) * a.row_bytes), static_cast<short>(0), rbytes,
+    // DMA of the workgroup's tile s (clamped to its last one, so every round issues U units
+    // per wave) into ring slot s % kRingSlots; rows past the matrix read as zero
+    auto dma = [&](int s) {
+        s = min(s, cnt - 1);
+        const int r0 = (static_cast<int>(blockIdx.x) + s * G) * k.R;
+        const int nrec = min(k.R, static_cast<int>(a.rows) - r0) * static_cast<int>(a.row_bytes);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(a.w + static_cast<long long>(r0) * a.row_bytes), static_cast<short>(0), nrec,
             kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(a.w + min(r0 + 2 * pr + 1, a.rows - 1) * a.row_bytes), static_cast<short>(0),
-            rbytes, kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(x), static_cast<short>(0), nch * 32, kBufferFlags);
-        const uint32_t vo = static_cast<uint32_t>(cl * B), vx = static_cast<uint32_t>(cl * 32);
-        float* out0 = &P[0][(2 * pr) * 8 * kFpPad + cl];
-        FpLoad<FMT> w0[kFpSlots], w1[kFpSlots];
-        u32x4_t xa[kFpSlots], xb[kFpSlots];
-        auto issue = [&](int s, FpLoad<FMT>& l0, FpLoad<FMT>& l1, u32x4_t& x0, u32x4_t& x1) {
-            const uint32_t so = static_cast<uint32_t>(s * kFpSeg * B), sx = static_cast<uint32_t>(s * kFpSeg * 32);
-            fp_load_chunk<FMT>(rs0, vo, so, l0);
-            fp_load_chunk<FMT>(rs1, vo, so, l1);
-            x0 = __builtin_amdgcn_raw_buffer_load_b128(rsx, vx, sx, 0);
-            x1 = __builtin_amdgcn_raw_buffer_load_b128(rsx, vx + 16, sx, 0);
-        };
-        auto produce = [&](int s, const FpLoad<FMT>& l0, const FpLoad<FMT>& l1, const u32x4_t& x0, const u32x4_t& x1) {
-            float xv[8];
+        char* slot = ring_lds + (s % kRingSlots) * k.slot_bytes;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xv[i] = __uint_as_float(x0[i]);
-                xv[4 + i] = __uint_as_float(x1[i]);
-            }
-            float v0[8], v1[8];
-            fp_decode<FMT>(l0, v0);
-            fp_decode<FMT>(l1, v1);
-            // chunks past the row were read as zero; their products are stored but never added
-            float* o = out0 + (s & 1) * (kFpRows * 8 * kFpPad);
-#pragma unroll
-            for (int L = 0; L < 8; ++L) {
-                o[L * kFpPad] = mul_rn(v0[L], xv[L]);
-                o[(8 + L) * kFpPad] = mul_rn(v1[L], xv[L]);
-            }
-            lds_barrier();
-        };
-        // round s: segment s into buffer s & 1 (the chain wave reads segment s - 1), then a
-        // barrier; nseg + 1 rounds.  Loads run kFpSlots - 1 segments ahead in kFpSlots register
-        // slots (the loads of rounds past the last segment re-read it: the count stays the same).
-#pragma unroll
-        for (int u = 0; u < kFpSlots - 1; ++u) issue(min(u, nseg - 1), w0[u], w1[u], xa[u], xb[u]);
-        for (int s0 = 0;; s0 += kFpSlots) {  // exits only through the break: the back-edge is steady state
-            bool done = false;
-#pragma unroll
-            for (int u = 0; u < kFpSlots; ++u) {
-                const int sl = (u + kFpSlots - 1) % kFpSlots;
-                issue(min(s0 + u + kFpSlots - 1, nseg - 1), w0[sl], w1[sl], xa[sl], xb[sl]);
-                produce(s0 + u, w0[u], w1[u], xa[u], xb[u]);
-                if (s0 + u + 1 >= nseg) {
-                    done = true;
-                    break;
-                }
-            }
-            if (done) break;
+        for (int i = 0; i < U; ++i) {
+            const int u = wave + 4 * i;
+            buffer_load_lds16(rs, slot + 1024 * u, static_cast<uint32_t>(16 * lane), static_cast<uint32_t>(1024 * u));
         }
-        lds_barrier();  // round nseg: the chain wave adds the last segment
-        return;
-    }
-
-    // the chain wave: lane = 8 * row + L
-    const int lane = t - kFpProducers;
-    const int rr = lane >> 3, L = lane & 7;
-    float acc = 0.0f;
-    lds_barrier();  // round 0
-    for (int s = 0; s < nseg; ++s) {
-        const float4* pr = reinterpret_cast<const float4*>(&P[s & 1][lane * kFpPad]);
-        const int n = min(kFpSeg, nch - s * kFpSeg);
+    };
+    // x first, awaited before any DMA is in flight: the compiler counts its loads but not the
+    // DMAs, and a wait for x inside the loop would also wait for every tile in flight
+    typename Pol::Lane pl;
+    Pol::prep(pl, x, pc);
+    wait_vmcnt<0>();
 #pragma unroll
-        for (int i = 0; i < kFpSeg / 4; ++i) {
-            const float4 v = pr[i];
-            if (4 * i + 0 < n) acc = add_rn(acc, v.x);
-            if (4 * i + 1 < n) acc = add_rn(acc, v.y);
-            if (4 * i + 2 < n) acc = add_rn(acc, v.z);
-            if (4 * i + 3 < n) acc = add_rn(acc, v.w);
-        }
-        lds_barrier();  // round s + 1
-    }
-    // HSum in lane order over the row's 8 lanes
-    const int base = lane & ~7;
-    float sum = 0.0f;
+    for (int s = 0; s < kRingSlots - 1; ++s) dma(s);
+    for (int s = 0; s < cnt; ++s) {
+        wait_vmcnt<(kRingSlots - 2) * U>();  // this wave's units of tile s have landed
+        lds_barrier();                       // everyone's have; slot (s - 1) % kRingSlots is free
+        dma(s + kRingSlots - 1);
+        V v[RPT][Pol::kLoads];
+        ring_read<Pol, RPT>(ring_lds + (s % kRingSlots) * k.slot_bytes, static_cast<int>(a.row_bytes), g, pc, v);
 #pragma unroll
-    for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(acc, base + l, 64));
-    const long long row = r0 + rr;
-    if constexpr (FMT == QR_FMT_F16) {
-        if (!isfinite(sum) && row < a.rows) {
-            // exact decode of the row's lane chain (HalfBitsToFloat, DotKernels.cs:86-100)
-            const uint8_t* w = a.w + row * a.row_bytes;
-            float e = 0.0f;
-            for (int c = 0; c < nch; ++c) {
-                const int k = 8 * c + L;
-                e = add_rn(e, mul_rn(f16_dot_decode(*reinterpret_cast<const uint16_t*>(w + 2 * k)), x[k]));
-            }
-            sum = 0.0f;
-#pragma unroll
-            for (int l = 0; l < 8; ++l) sum = add_rn(sum, __shfl(e, base + l, 64));
+        for (int r = 0; r < RPT; ++r) {
+            float t0, t1;
+            Pol::terms(pl, v[r], t0, t1);
+            if (active)
+                *reinterpret_cast<float2*>(terms + ((s * k.R) + g * RPT + r) * k.tstride + 2 * pc) = make_float2(t0, t1);
         }
     }
-    if (L == 0 && row < a.rows) a.y[static_cast<long long>(q) * a.rows + row] = sum;
+    wait_dma();
+    __syncthreads();
+    const int nt = 2 * k.P;
+    for (int i = t; i < cnt * k.R; i += blockDim.x) {
+        const int s = i / k.R, r = i - s * k.R;
+        const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
+        if (row >= a.rows) continue;
+        const float4* tr = reinterpret_cast<const float4*>(terms + i * k.tstride);
+        float sum = 0.0f;
+        for (int c0 = 0; c0 < nt; c0 += 16) {
+            float4 vv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vv[c] = tr[min(c0 / 4 + c, (nt - 1) / 4)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int base = c0 + 4 * c;
+                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
+                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
+                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
+                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
+            }
+        }
+        a.y[static_cast<long long>(q) * a.rows + row] = sum;
+    }
 }
 
-// Single-wave form of the same order: a workgroup is one wave and R <= 8 rows, lane 8r + L
-// the chain (row r, lane L).  The wave streams its rows in segments of 1 KiB per row through a
+// ---- F32 / F16 / BF16 (DotF32 order, DotKernels.cs:52-100).  Row r's lane L accumulates
+// k = 8c + L over the chunks c in order, so every row is 8 serial chains.  A workgroup is one
+// wave and R <= 8 rows, lane 8r + L the chain (row r, lane L).  The wave streams its rows in segments of 1 KiB per row through a
 // ring of kFwSlots LDS slots filled by direct-to-LDS buffer loads (kFwSlots - 1 segments in
 // flight; completion awaited with explicit vmcnt waits), and each lane walks its chain over
 // the chunks of a segment: weight, x, product, add.  No barrier, no register prefetch.
@@ -1245,36 +1107,63 @@ MvLayout mv_layout(const MatVecArgs& a) {
     return L;
 }
 
-// Q4_K rows through matvec_q4k_kernel: weights and x 16-byte aligned (a Q4_K row is 144-byte
-// blocks, so rows stay aligned when the base is) and the term rows within 64 KiB of LDS.
-#ifndef QR_MV_Q4K_RPT
-#define QR_MV_Q4K_RPT 0
-#endif
+constexpr int kBlkRptQ4k = 2;  // Q4_K rows per thread and tile (Q8_0: 1, its 17 loads a row)
+constexpr int kBlkWgPerCu = 3;
 
-bool q4k_config(const MatVecArgs& a, MvQ4k* k, int* rpt_out) {
-    if (a.fmt != QR_FMT_Q4_K || reinterpret_cast<uintptr_t>(a.w) % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
-        a.row_bytes % 16)
-        return false;
-    k->P = a.cols / 64;
-    k->tpg = std::min(kMvThreads, (k->P + 63) / 64 * 64);
-    k->rg = kMvThreads / k->tpg;
-    // rows per thread: halved while that leaves fewer than 1024 workgroups
-    int rpt = 4;
-    while (rpt > 1 && (a.rows + static_cast<long long>(k->rg) * rpt - 1) / (static_cast<long long>(k->rg) * rpt) < 1024)
-        rpt >>= 1;
-    if (QR_MV_Q4K_RPT) rpt = QR_MV_Q4K_RPT;
-    k->R = k->rg * rpt;
-    k->tstride = (2 * k->P + 3) / 4 * 4 + 4;
-    *rpt_out = rpt;
-    return static_cast<size_t>(k->R) * k->tstride * 4 <= 64 * 1024;
+template <int U>
+hipError_t ring_launch_q8(const MatVecArgs& a, const MvRing& k, dim3 grid, size_t lds, hipStream_t stream) {
+    static bool attr = false;  // dynamic LDS above 64 KiB must be allowed per kernel
+    if (lds > 64 * 1024 && !attr) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_blk_ring<PolQ8, 1, U>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((matvec_blk_ring<PolQ8, 1, U>), grid, dim3(kMvThreads), lds, stream, a, k);
+    return hipGetLastError();
 }
 
-#ifndef QR_MV_BLKP_RPT
-#define QR_MV_BLKP_RPT 2
-#endif
-#ifndef QR_MV_BLKP_WGCU
-#define QR_MV_BLKP_WGCU 3
-#endif
+// The ring form, used for Q8_0 (Q4_K is VALU-bound and measures faster in the persistent
+// form): block pairs, rows of at most 256 pairs (16384 columns), tiles of at most 32 KiB;
+// false when the shape does not fit.
+bool blk_ring_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
+    if (a.fmt != QR_FMT_Q8_0 || reinterpret_cast<uintptr_t>(a.x) % 16 || a.cols % 64 ||
+        reinterpret_cast<uintptr_t>(a.w) % 4 || a.row_bytes % 4)
+        return false;
+    MvRing k{};
+    k.P = a.cols / 64;
+    if (k.P > 256) return false;
+    k.tpg = k.P <= 64 ? 64 : k.P <= 128 ? 128 : 256;  // four waves always: U units per wave per tile
+    k.rg = kMvThreads / k.tpg;
+    k.R = k.rg;
+    const long long tile = static_cast<long long>(k.R) * a.row_bytes;
+    int U = static_cast<int>((tile + 4095) / 4096);
+    if (U > 8) return false;
+    if (U == 7) U = 8;
+    k.slot_bytes = 4096 * U;
+    k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
+    k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
+    if (a.rows >= (1LL << 31) - k.R) return false;
+    // workgroups: two per CU when the LDS allows, the terms of all of a workgroup's tiles kept
+    int G = std::min(k.ntiles, 512);
+    size_t lds = 0;
+    for (;; G = std::min(k.ntiles, G * 2)) {
+        const int tpw = (k.ntiles + G - 1) / G;
+        lds = static_cast<size_t>(kRingSlots) * k.slot_bytes + static_cast<size_t>(tpw) * k.R * k.tstride * 4;
+        if (lds <= 80 * 1024 || G == k.ntiles) break;
+    }
+    if (lds > 160 * 1024) return false;
+    const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
+    switch (U) {
+    case 1: case 2: *err = ring_launch_q8<2>(a, k, grid, lds, stream); break;
+    case 3: *err = ring_launch_q8<3>(a, k, grid, lds, stream); break;
+    case 4: *err = ring_launch_q8<4>(a, k, grid, lds, stream); break;
+    case 5: *err = ring_launch_q8<5>(a, k, grid, lds, stream); break;
+    case 6: *err = ring_launch_q8<6>(a, k, grid, lds, stream); break;
+    default: *err = ring_launch_q8<8>(a, k, grid, lds, stream); break;
+    }
+    return true;
+}
 
 // The persistent form for Q4_K (64-column items: rows of at most 512 items, 32768 columns) and
 // Q8_0 (block pairs: whole pairs and 4-byte aligned rows): false when the shape does not fit or
@@ -1290,31 +1179,22 @@ bool blk_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* 
     k.tpg = (k.P + 63) / 64 * 64;
     k.rg = std::max(1, kMvThreads / k.tpg);
     // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts
-    const int rpt = q4k ? QR_MV_BLKP_RPT : 1;
+    const int rpt = q4k ? kBlkRptQ4k : 1;
     k.R = k.rg * rpt;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
     k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
     if (static_cast<long long>(k.R) * a.row_bytes >= (1LL << 31) || a.rows >= (1LL << 31) - k.R) return false;
     const int threads = k.rg * k.tpg;
-    const int wg_per_cu = std::max(1, QR_MV_BLKP_WGCU * 256 / threads);
+    const int wg_per_cu = std::max(1, kBlkWgPerCu * 256 / threads);
     int G = std::min(k.ntiles, 256 * wg_per_cu);
     const int tpw = (k.ntiles + G - 1) / G;
     const size_t lds = static_cast<size_t>(tpw) * k.R * k.tstride * 4;
     if (lds > 64 * 1024) return false;
     const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
-    if (q4k) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, QR_MV_BLKP_RPT>), grid, dim3(threads), lds, stream, a, k);
+    if (q4k) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, kBlkRptQ4k>), grid, dim3(threads), lds, stream, a, k);
     else hipLaunchKernelGGL((matvec_blk_persistent<PolQ8, 1>), grid, dim3(threads), lds, stream, a, k);
     *err = hipGetLastError();
     return true;
-}
-
-hipError_t launch_q4k(const MatVecArgs& a, const MvQ4k& k, int rpt, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(k.R) * k.tstride * 4;
-    const dim3 grid(static_cast<unsigned>((a.rows + k.R - 1) / k.R), static_cast<unsigned>(a.nq));
-    if (rpt == 4) hipLaunchKernelGGL(matvec_q4k_kernel<4>, grid, dim3(kMvThreads), lds, stream, a, k);
-    else if (rpt == 2) hipLaunchKernelGGL(matvec_q4k_kernel<2>, grid, dim3(kMvThreads), lds, stream, a, k);
-    else hipLaunchKernelGGL(matvec_q4k_kernel<1>, grid, dim3(kMvThreads), lds, stream, a, k);
-    return hipGetLastError();
 }
 
 template <int FMT>
@@ -1344,22 +1224,14 @@ bool matvec_shape_ok(int fmt, int cols) {
     return !fp || cols % 8 == 0;
 }
 
-// The producer/consumer fp form needs 16-byte aligned rows and x.
+// The single-wave fp form needs 16-byte aligned rows and x.
 template <int FMT>
 hipError_t launch_fp(const MatVecArgs& a, hipStream_t stream) {
     if (reinterpret_cast<uintptr_t>(a.w) % 16 || a.row_bytes % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
         a.cols % 8)
         return launch_fmt<FMT>(a, stream);
-#ifndef QR_MV_FP_FORM
-#define QR_MV_FP_FORM 1
-#endif
-    if (QR_MV_FP_FORM == 1) {
-        const dim3 grid(static_cast<unsigned>((a.rows + 7) / 8), static_cast<unsigned>(a.nq));
-        hipLaunchKernelGGL((matvec_fp_wave<FMT, 8>), grid, dim3(64), 0, stream, a);
-        return hipGetLastError();
-    }
-    const dim3 grid(static_cast<unsigned>((a.rows + kFpRows - 1) / kFpRows), static_cast<unsigned>(a.nq));
-    hipLaunchKernelGGL(matvec_fp_kernel<FMT>, grid, dim3(kFpThreads), 0, stream, a);
+    const dim3 grid(static_cast<unsigned>((a.rows + 7) / 8), static_cast<unsigned>(a.nq));
+    hipLaunchKernelGGL((matvec_fp_wave<FMT, 8>), grid, dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -1372,15 +1244,13 @@ hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
     case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
     case QR_FMT_Q8_0: {
         hipError_t e;
+        if (blk_ring_launch(a, stream, &e)) return e;
         if (blk_persistent_launch(a, stream, &e)) return e;
         return launch_fmt<QR_FMT_Q8_0>(a, stream);
     }
     case QR_FMT_Q4_K: {
         hipError_t e;
         if (blk_persistent_launch(a, stream, &e)) return e;
-        MvQ4k k;
-        int rpt;
-        if (q4k_config(a, &k, &rpt)) return launch_q4k(a, k, rpt, stream);
         return launch_fmt<QR_FMT_Q4_K>(a, stream);
     }
     case QR_FMT_Q6_K: return launch_fmt<QR_FMT_Q6_K>(a, stream);
