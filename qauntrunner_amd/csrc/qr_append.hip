@@ -87,6 +87,8 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherArgs a) {
 // the same dims of V, q heads are rotated in place.  Products and sums are separately
 // rounded as in the reference (x0 c - x1 s, x0 s + x1 c).
 constexpr int kRopeRows = 1;
+constexpr int kVTileTpt = 8;       // V tile: tokens per thread (one 16-byte chunk per dim)
+constexpr int kRopeThreads = 256;  // threads per position workgroup and per V tile
 
 // 4 consecutive dims of one cache row: one 16- or 8-byte store when the plane is
 // token-major, element stores when it is dims-major.
@@ -111,12 +113,71 @@ __device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g,
     for (int e = 0; e < 4; ++e) base[g.offset(phys, plane, kvh, slot, d + e)] = b[e];
 }
 
+// A dims-major V plane keeps one dim of kPageTokens tokens contiguous, so a position's V
+// row lands as 2-byte stores 2*kPageTokens bytes apart.  V tiles write it instead: a
+// workgroup owns an aligned run of T tokens of one kv head (T divides kPageTokens, so
+// the run lies in one page), each thread 2 dims x TPT consecutive tokens, and a chunk of
+// 8 tokens of one dim is one 16-byte store.  Source rows outside [pos0, pos0 + n) are
+// clamped loads whose values are never stored; chunks at the ends of the range store
+// only their in-range tokens.
+__host__ __device__ constexpr int v_tile_tokens(int head_dim, int tpt) { return 2 * kRopeThreads / head_dim * tpt; }
+
+template <int TPT>
+__device__ __forceinline__ void v_tile_store(const AppendArgs& g, int vb) {
+    static_assert(TPT % 8 == 0, "whole 16-byte chunks");
+    const int D = g.geom.head_dim;
+    const int pairs = D >> 1;  // 32 or 64
+    const int T = v_tile_tokens(D, TPT);
+    const int kvh = vb % g.geom.kv_heads;
+    const int tbase = (g.pos0 / T + vb / g.geom.kv_heads) * T;
+    const int dp = threadIdx.x & (pairs - 1);
+    const int t0 = tbase + (threadIdx.x / pairs) * TPT;
+    const float* src = static_cast<const float*>(g.src[1]) + kvh * D + 2 * dp;
+    float2 v[TPT];
+#pragma unroll
+    for (int k = 0; k < TPT; ++k) {
+        const int r = min(max(t0 + k - g.pos0, 0), g.n - 1);
+        v[k] = *reinterpret_cast<const float2*>(src + static_cast<long long>(r) * g.src_stride);
+    }
+    const long long phys = g.page_table[tbase >> kPageShift];
+    const int slot0 = t0 & (kPageTokens - 1);
+    const bool whole = t0 >= g.pos0 && t0 + TPT <= g.pos0 + g.n;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        uint16_t b[TPT];
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) {
+            const float x = e ? v[k].y : v[k].x;
+            b[k] = g.dtype == QR_DTYPE_F16 ? f32_to_f16_bits_ref(x) : f32_to_bf16_bits_ref(x);
+        }
+        uint16_t* p = static_cast<uint16_t*>(g.pool) + g.geom.offset(phys, 1, kvh, slot0, 2 * dp + e);
+        if (whole) {
+#pragma unroll
+            for (int c = 0; c < TPT / 8; ++c) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = b[8 * c + 2 * j] | (static_cast<uint32_t>(b[8 * c + 2 * j + 1]) << 16);
+                *reinterpret_cast<uint4*>(p + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < TPT; ++k)
+                if (t0 + k >= g.pos0 && t0 + k < g.pos0 + g.n) p[k] = b[k];
+        }
+    }
+}
+
 // Same work with the loads of all of a thread's items issued before the cos/sin of the
 // position are computed: the libm calls overlap the memory latency instead of preceding it.
-// IPT = items per thread (heads * head_dim / 8 <= 256 * IPT).
-template <int IPT>
-__global__ void __launch_bounds__(256) rope_append_items_kernel(const RopeAppendArgs a) {
+// IPT = items per thread (heads * head_dim / 8 <= kRopeThreads * IPT).  With TPT > 0 the first
+// nv workgroups are V tiles and the position workgroups leave V alone.
+template <int IPT, int TPT>
+__global__ void __launch_bounds__(kRopeThreads) rope_append_items_kernel(const RopeAppendArgs a, int nv) {
     const AppendArgs& g = a.app;
+    if (TPT > 0 && static_cast<int>(blockIdx.x) < nv) {
+        v_tile_store<TPT ? TPT : 8>(g, blockIdx.x);
+        return;
+    }
     const int D = g.geom.head_dim;
     const int half = D >> 1;
     const int kv_heads = g.geom.kv_heads;
@@ -124,23 +185,25 @@ __global__ void __launch_bounds__(256) rope_append_items_kernel(const RopeAppend
     const int heads = kv_heads + q_heads;
     const int per_head = half / 4;
     const int nitems = heads * per_head;
-    const long long row = blockIdx.x;  // one position per workgroup
+    const long long row = static_cast<int>(blockIdx.x) - (TPT > 0 ? nv : 0);  // one position per workgroup
     float4 x0[IPT], x1[IPT], w0[IPT], w1[IPT];
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
-        const int it = min(static_cast<int>(threadIdx.x) + 256 * k, nitems - 1);  // past the end: a valid item, not stored
+        const int it = min(static_cast<int>(threadIdx.x) + kRopeThreads * k, nitems - 1);  // past the end: a valid item, not stored
         const int h = it / per_head;
         const int d = 4 * (it - h * per_head);
         const float* src = h < kv_heads ? static_cast<const float*>(g.src[0]) + row * g.src_stride + h * D
                                         : a.q + row * a.q_width + (h - kv_heads) * D;
         x0[k] = *reinterpret_cast<const float4*>(src + d);
         x1[k] = *reinterpret_cast<const float4*>(src + d + half);
-        const float* v = static_cast<const float*>(g.src[1]) + row * g.src_stride + min(h, kv_heads - 1) * D;
-        w0[k] = *reinterpret_cast<const float4*>(v + d);
-        w1[k] = *reinterpret_cast<const float4*>(v + d + half);
+        if (TPT == 0) {
+            const float* v = static_cast<const float*>(g.src[1]) + row * g.src_stride + min(h, kv_heads - 1) * D;
+            w0[k] = *reinterpret_cast<const float4*>(v + d);
+            w1[k] = *reinterpret_cast<const float4*>(v + d + half);
+        }
     }
     __shared__ float cs[2][kMaxRopeHalf];
-    for (int i = threadIdx.x; i < half; i += 256) {
+    for (int i = threadIdx.x; i < half; i += kRopeThreads) {
         const float ang = mul_rn(static_cast<float>(g.pos0 + row), a.freq[i]);
         cs[0][i] = cosf(ang);
         cs[1][i] = sinf(ang);
@@ -151,7 +214,7 @@ __global__ void __launch_bounds__(256) rope_append_items_kernel(const RopeAppend
     const int slot = t & (kPageTokens - 1);
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
-        const int it = threadIdx.x + 256 * k;
+        const int it = threadIdx.x + kRopeThreads * k;
         if (it >= nitems) break;
         const int h = it / per_head;
         const int d = 4 * (it - h * per_head);
@@ -168,9 +231,11 @@ __global__ void __launch_bounds__(256) rope_append_items_kernel(const RopeAppend
         if (h < kv_heads) {
             store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d, y0);
             store4(g.pool, g.dtype, g.geom, phys, 0, h, slot, d + half, y1);
-            const float v0[4] = {w0[k].x, w0[k].y, w0[k].z, w0[k].w}, v1[4] = {w1[k].x, w1[k].y, w1[k].z, w1[k].w};
-            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d, v0);
-            store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d + half, v1);
+            if (TPT == 0) {
+                const float v0[4] = {w0[k].x, w0[k].y, w0[k].z, w0[k].w}, v1[4] = {w1[k].x, w1[k].y, w1[k].z, w1[k].w};
+                store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d, v0);
+                store4(g.pool, g.dtype, g.geom, phys, 1, h, slot, d + half, v1);
+            }
         } else {
             float* q = a.q + row * a.q_width + (h - kv_heads) * D;
             *reinterpret_cast<float4*>(q + d) = make_float4(y0[0], y0[1], y0[2], y0[3]);
@@ -269,18 +334,33 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
     const int D = a.app.geom.head_dim;
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
-    const int ipt = (heads * (D / 8) + 255) / 256;
-    const dim3 grid(static_cast<unsigned>(a.app.n));
+    const int ipt = (heads * (D / 8) + kRopeThreads - 1) / kRopeThreads;
+    // V tiles: 16-bit dims-major V plane (head_dim 64 or 128), kVTileTpt tokens per thread
+    const bool tiles = a.app.geom.v_dims_major && a.app.geom.planes == 2 && (D == 64 || D == 128) &&
+                       a.app.dtype != QR_DTYPE_F32;
+    int nv = 0;
+    if (tiles) {
+        const int T = v_tile_tokens(D, kVTileTpt);
+        nv = ((a.app.pos0 + a.app.n - 1) / T - a.app.pos0 / T + 1) * a.app.geom.kv_heads;
+    }
+    const dim3 grid(static_cast<unsigned>(a.app.n + nv));
+#define QR_ROPE_ITEMS(I)                                                                               \
+    do {                                                                                               \
+        if (tiles) hipLaunchKernelGGL((rope_append_items_kernel<I, kVTileTpt>), grid, dim3(kRopeThreads), 0, stream, a, nv); \
+        else hipLaunchKernelGGL((rope_append_items_kernel<I, 0>), grid, dim3(kRopeThreads), 0, stream, a, 0);             \
+    } while (0)
     switch (ipt) {
-    case 1: hipLaunchKernelGGL(rope_append_items_kernel<1>, grid, dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL(rope_append_items_kernel<2>, grid, dim3(256), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL(rope_append_items_kernel<3>, grid, dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL(rope_append_items_kernel<4>, grid, dim3(256), 0, stream, a); break;
-    case 5: case 6: hipLaunchKernelGGL(rope_append_items_kernel<6>, grid, dim3(256), 0, stream, a); break;
-    case 7: case 8: hipLaunchKernelGGL(rope_append_items_kernel<8>, grid, dim3(256), 0, stream, a); break;
+    case 1: QR_ROPE_ITEMS(1); break;
+    case 2: QR_ROPE_ITEMS(2); break;
+    case 3: QR_ROPE_ITEMS(3); break;
+    case 4: QR_ROPE_ITEMS(4); break;
+    case 5: QR_ROPE_ITEMS(5); break;
+    case 6: QR_ROPE_ITEMS(6); break;
+    case 7: case 8: QR_ROPE_ITEMS(8); break;
     default:
         hipLaunchKernelGGL(rope_append_kernel, dim3((a.app.n + kRopeRows - 1) / kRopeRows), dim3(256), 0, stream, a);
     }
+#undef QR_ROPE_ITEMS
     return hipGetLastError();
 }
 

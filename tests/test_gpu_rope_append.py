@@ -94,6 +94,32 @@ def test_rope_append_dev_bulk(gpu, dtype):
     assert same >= 0.99
 
 
+@pytest.mark.parametrize("dtype,D", [("f16", 128), ("bf16", 128), ("f16", 64), ("bf16", 64)])
+def test_rope_append_dev_ragged_ranges(gpu, dtype, D):
+    """Device appends at unaligned positions and lengths (single rows, runs that end
+    mid-chunk, runs across page boundaries): every V row read back equals its 16-bit
+    rounding, so no append overwrote a neighbour's slots, and K agrees as in the bulk test."""
+    import torch
+    heads, kv_heads, theta = 4, 2, 10000.0
+    spans = [(0, 37), (37, 1), (38, 3), (41, 300), (341, 171), (512, 8), (520, 1), (521, 250)]
+    total = spans[-1][0] + spans[-1][1]
+    Q = normal(340 + D, (total, heads * D))
+    K, V = normal(341 + D, (total, kv_heads * D)), normal(342 + D, (total, kv_heads * D))
+    dev = torch.device("cuda")
+    with qr.PagedKvCache(1, heads, kv_heads, D, total, kv_dtype=dtype) as kv:
+        for pos0, n in spans:
+            qd = torch.from_numpy(Q[pos0:pos0 + n]).to(dev)
+            kv.AppendRopeDev(0, pos0, qd, torch.from_numpy(K[pos0:pos0 + n]).to(dev),
+                             torch.from_numpy(V[pos0:pos0 + n]).to(dev), theta)
+        torch.cuda.synchronize()
+        kr, vr = kv.Read(0, 0, total)
+    enc = oracle.f32_to_f16 if dtype == "f16" else oracle.f32_to_bf16
+    bad = np.argwhere(vr != enc(V))
+    assert bad.size == 0, f"V differs at (position, column) {tuple(bad[0])}, {len(bad)} elements"
+    kw = rope_ref(K, D, 0, theta)
+    assert np.mean(kr == enc(kw)) >= 0.99
+
+
 def test_rope_append_then_attention(gpu):
     """Decode over rows appended through the fused step equals the oracle's attention over
     oracle-rotated rows (fp32 accumulation tolerance)."""
