@@ -321,6 +321,43 @@ __device__ __forceinline__ void q4k_pair_terms(const u32x4_t h, const u32x4_t qa
 // while the current tile is computed (two register buffers, the loop unrolled by two so that
 // each half waits only for its own loads), every tile's terms stay in LDS, and the in-order
 // sums of all the workgroup's rows run at the end.  blockDim = rg * tpg threads.
+// x row pitch in LDS: 64 values and 4 floats of padding
+constexpr int kXRow = 68;
+
+// In-order sum (left to right, from +0) of a row's nt terms (nt even, 16-byte aligned) in
+// LDS.  Groups of 32 terms: the loads of the next group are issued before the adds of the
+// current one (clamped to the row, so every iteration issues the same loads), so the chain
+// of dependent adds waits for LDS once per row instead of once per group.
+__device__ __forceinline__ float ordered_row_sum(const float* tr, int nt) {
+    const float4* t4 = reinterpret_cast<const float4*>(tr);
+    const int n4 = nt >> 2;
+    const int last = max(n4 - 1, 0);
+    float sum = 0.0f;
+    auto add4 = [&](const float4 v) { sum = add_rn(add_rn(add_rn(add_rn(sum, v.x), v.y), v.z), v.w); };
+    auto load8 = [&](float4 (&v)[8], int g0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = t4[min(g0 + j, last)];
+    };
+    float4 a[8], b[8];
+    int g = 0;
+    load8(a, 0);
+    for (;;) {
+        if (g + 8 > n4) break;
+        load8(b, g + 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) add4(a[j]);
+        g += 8;
+        if (g + 8 > n4) break;
+        load8(a, g + 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) add4(b[j]);
+        g += 8;
+    }
+    for (; g < n4; ++g) add4(t4[g]);  // the last n4 % 8 groups
+    if (nt & 2) sum = add_rn(add_rn(sum, tr[nt - 2]), tr[nt - 1]);
+    return sum;
+}
+
 struct MvBlkP {
     int P, tpg, rg, R, tstride;
     int ntiles;   // ceil(rows / R)
@@ -342,9 +379,9 @@ struct PolQ4K {
         o[1] = b + 16 + 32 * (pc & 3);
         o[2] = o[1] + 16;
     }
-    __device__ static void prep(Lane& l, const float* x, int pc) {
+    __device__ static void prep(Lane& l, const float* xi, int pc) {  // xi: the item's 64 values
         l.j = pc & 3;
-        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+        const float4* x4 = reinterpret_cast<const float4*>(xi);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const float4 f = x4[i];
@@ -378,8 +415,8 @@ struct PolQ8 {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) o[i] = static_cast<uint32_t>(68 * pc + 4 * i);
     }
-    __device__ static void prep(Lane& l, const float* x, int pc) {
-        const float4* x4 = reinterpret_cast<const float4*>(x + 64 * pc);
+    __device__ static void prep(Lane& l, const float* xi, int) {  // xi: the item's 64 values
+        const float4* x4 = reinterpret_cast<const float4*>(xi);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const float4 f = x4[i];
@@ -468,8 +505,17 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
     V vA[RPT][Pol::kLoads], vB[RPT][Pol::kLoads];
     int it = blockIdx.x;
     blk_load<Pol, RPT>(a, k, it, off, vA);
+    // x reaches the threads through LDS: one coalesced copy per workgroup (every thread of
+    // every workgroup reading its 64 values from global memory made all CUs hit the same
+    // lines of L2 at once), 64-value rows padded by 4 floats so that the rows the lanes read
+    // start on distinct banks.  The area is the terms' area, written only after the barrier.
+    float* xl = reinterpret_cast<float*>(mv_lds);
+    for (int i = 4 * t; i < a.cols; i += 4 * static_cast<int>(blockDim.x))
+        *reinterpret_cast<float4*>(xl + i + 4 * (i >> 6)) = *reinterpret_cast<const float4*>(x + i);
+    __syncthreads();
     typename Pol::Lane lane;
-    Pol::prep(lane, x, pc);
+    Pol::prep(lane, xl + kXRow * pc, pc);
+    __syncthreads();
     auto compute = [&](const V (&v)[RPT][Pol::kLoads], int slot) {
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
@@ -500,22 +546,7 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
         const int s = i / k.R, r = i - s * k.R;
         const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
         if (row >= a.rows) continue;
-        const float4* tr = reinterpret_cast<const float4*>(terms + i * k.tstride);
-        float sum = 0.0f;
-        for (int c0 = 0; c0 < nt; c0 += 16) {
-            float4 vv[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vv[c] = tr[min(c0 / 4 + c, (nt - 1) / 4)];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int base = c0 + 4 * c;
-                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
-                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
-                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
-                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
-            }
-        }
-        a.y[static_cast<long long>(q) * a.rows + row] = sum;
+        a.y[static_cast<long long>(q) * a.rows + row] = ordered_row_sum(terms + i * k.tstride, nt);
     }
 }
 
@@ -584,7 +615,7 @@ __global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
     // x first, awaited before any DMA is in flight: the compiler counts its loads but not the
     // DMAs, and a wait for x inside the loop would also wait for every tile in flight
     typename Pol::Lane pl;
-    Pol::prep(pl, x, pc);
+    Pol::prep(pl, x + 64 * pc, pc);
     wait_vmcnt<0>();
 #pragma unroll
     for (int s = 0; s < kRingSlots - 1; ++s) dma(s);
@@ -609,22 +640,7 @@ __global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
         const int s = i / k.R, r = i - s * k.R;
         const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
         if (row >= a.rows) continue;
-        const float4* tr = reinterpret_cast<const float4*>(terms + i * k.tstride);
-        float sum = 0.0f;
-        for (int c0 = 0; c0 < nt; c0 += 16) {
-            float4 vv[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vv[c] = tr[min(c0 / 4 + c, (nt - 1) / 4)];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int base = c0 + 4 * c;
-                if (base + 0 < nt) sum = add_rn(sum, vv[c].x);
-                if (base + 1 < nt) sum = add_rn(sum, vv[c].y);
-                if (base + 2 < nt) sum = add_rn(sum, vv[c].z);
-                if (base + 3 < nt) sum = add_rn(sum, vv[c].w);
-            }
-        }
-        a.y[static_cast<long long>(q) * a.rows + row] = sum;
+        a.y[static_cast<long long>(q) * a.rows + row] = ordered_row_sum(terms + i * k.tstride, nt);
     }
 }
 
@@ -1108,7 +1124,7 @@ MvLayout mv_layout(const MatVecArgs& a) {
 }
 
 constexpr int kBlkRptQ4k = 2;  // Q4_K rows per thread and tile (Q8_0: 1, its 17 loads a row)
-constexpr int kBlkWgPerCu = 3;
+constexpr int kBlkWgPerCu = 2;  // workgroups of 256 threads per CU (measured: 1 and 3 slower for Q4_K)
 
 template <int U>
 hipError_t ring_launch_q8(const MatVecArgs& a, const MvRing& k, dim3 grid, size_t lds, hipStream_t stream) {
@@ -1178,20 +1194,40 @@ bool blk_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* 
     if (k.P > 512) return false;
     k.tpg = (k.P + 63) / 64 * 64;
     k.rg = std::max(1, kMvThreads / k.tpg);
-    // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts
-    const int rpt = q4k ? kBlkRptQ4k : 1;
+    // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts;
+    // Q4_K matrices with fewer than 512 tiles of kBlkRptQ4k rows per thread take one row per
+    // thread (twice the tiles: their runtime is the latency of a workgroup's few tiles)
+    int rpt = 1;
+    if (q4k) rpt = (a.rows + k.rg * kBlkRptQ4k - 1) / (k.rg * kBlkRptQ4k) < 512 ? 1 : kBlkRptQ4k;
     k.R = k.rg * rpt;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
     k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
     if (static_cast<long long>(k.R) * a.row_bytes >= (1LL << 31) || a.rows >= (1LL << 31) - k.R) return false;
     const int threads = k.rg * k.tpg;
     const int wg_per_cu = std::max(1, kBlkWgPerCu * 256 / threads);
+    // LDS: the terms of the workgroup's tiles, or the padded copy of x that precedes them;
+    // more workgroups (fewer tiles each) when the terms would not fit
     int G = std::min(k.ntiles, 256 * wg_per_cu);
-    const int tpw = (k.ntiles + G - 1) / G;
-    const size_t lds = static_cast<size_t>(tpw) * k.R * k.tstride * 4;
-    if (lds > 64 * 1024) return false;
+    size_t lds = 0;
+    for (;; G = std::min(k.ntiles, 2 * G)) {
+        const int tpw = (k.ntiles + G - 1) / G;
+        lds = std::max(static_cast<size_t>(tpw) * k.R * k.tstride * 4, static_cast<size_t>(k.P) * kXRow * 4);
+        if (lds <= 160 * 1024 || G == k.ntiles) break;
+    }
+    if (lds > 160 * 1024) return false;
+    const int which = q4k ? (rpt == 1 ? 1 : 2) : 0;
+    const void* fns[3] = {reinterpret_cast<const void*>(&matvec_blk_persistent<PolQ8, 1>),
+                          reinterpret_cast<const void*>(&matvec_blk_persistent<PolQ4K, 1>),
+                          reinterpret_cast<const void*>(&matvec_blk_persistent<PolQ4K, kBlkRptQ4k>)};
+    static bool attr[3] = {false, false, false};  // dynamic LDS above 64 KiB must be allowed per kernel
+    if (lds > 64 * 1024 && !attr[which]) {
+        *err = hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (*err != hipSuccess) return true;
+        attr[which] = true;
+    }
     const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
-    if (q4k) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, kBlkRptQ4k>), grid, dim3(threads), lds, stream, a, k);
+    if (which == 2) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, kBlkRptQ4k>), grid, dim3(threads), lds, stream, a, k);
+    else if (which == 1) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, 1>), grid, dim3(threads), lds, stream, a, k);
     else hipLaunchKernelGGL((matvec_blk_persistent<PolQ8, 1>), grid, dim3(threads), lds, stream, a, k);
     *err = hipGetLastError();
     return true;

@@ -68,6 +68,37 @@ def test_matvec_ragged_shapes(gpu, fmt, rows, cols, nq):
     assert_exact(got, want, f"{fmt} {rows}x{cols} nq{nq}")
 
 
+def assert_exact_nan(got, want, what):
+    """Bit-exact, except that any NaN matches any NaN (payloads are not compared)."""
+    g, w = got.reshape(-1), want.reshape(-1)
+    bad = np.flatnonzero((g != w) & ~(np.isnan(g) & np.isnan(w)))
+    assert bad.size == 0, f"{what}: {bad.size} of {g.size} differ, first at {bad[0]}: {g[bad[0]]!r} vs {w[bad[0]]!r}"
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_matvec_extreme_inputs(gpu, fmt):
+    """Vector 0 holds finite values at and above 2^103 (1.2e31, -3.0e38): the Q4_K kernel,
+    which otherwise takes its products from x prescaled by 2^24, falls back to unscaled x
+    for that vector's workgroups.  Vector 1 holds subnormals, tiny values and signed zeros;
+    vector 2 an infinity and a NaN.  Every row must still equal the oracle."""
+    rows, cols = 96, 4096
+    code = quant.FMT[fmt]
+    raw, _ = quant.random_rows(code, rows, cols, 60 + code, 0.05)
+    x = normal(61, (3, cols))
+    x[0, [5, 700, 4000]] = [np.float32(1.2e31), np.float32(-3.0e38), np.float32(2.0 ** 103)]
+    x[1, [0, 1, 2, 3, 33, 64, 300]] = [1e-40, -1e-45, 0.0, -0.0, 1e-38, -2e-39, 5e-30]
+    x[2, [17, 2049]] = [np.inf, np.nan]
+    y = torch.empty((3, rows), dtype=torch.float32, device="cuda")
+    qr.matvec_dev(dev(raw.reshape(-1)), code, rows, cols, dev(x), y)
+    torch.cuda.synchronize()
+    with np.errstate(all="ignore"):
+        want = np.stack([oracle.matvec(code, raw, cols, x[b]) for b in range(3)])
+    got = y.cpu().numpy()
+    for b in range(3):
+        assert_exact_nan(got[b], want[b], f"{fmt} vector {b}")
+    assert np.any(~np.isfinite(want[0])) or np.all(np.abs(want[0]) > 1e20)
+
+
 def test_matvec_f16_exponent_31_like_the_reference(gpu):
     """Halves with exponent 31 decode as finite 2^16-scale values in DotF16's vector path."""
     rows, cols = 4, 64
