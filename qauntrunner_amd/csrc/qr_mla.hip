@@ -482,35 +482,55 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
         l[nt] += __shfl_xor(l[nt], 16);
         l[nt] += __shfl_xor(l[nt], 32);
     }
+    if (p.splits == 1) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int head = hg * kMHeads + 16 * nt + l16;
-        if (head >= p.heads) continue;
-        const int dim0 = 128 * wave + 4 * q4;
-        if (p.splits == 1) {
-            float* out = p.u + static_cast<size_t>(head) * KL + dim0;
+        for (int nt = 0; nt < 2; ++nt) {
+            const int head = hg * kMHeads + 16 * nt + l16;
+            if (head >= p.heads) continue;
+            float* out = p.u + static_cast<size_t>(head) * KL + 128 * wave + 4 * q4;
             const float inv = 1.f / l[nt];
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
                 *reinterpret_cast<float4*>(out + 16 * dt) =
                     make_float4(acc[nt][dt][0] * inv, acc[nt][dt][1] * inv, acc[nt][dt][2] * inv, acc[nt][dt][3] * inv);
-        } else {
-            // normalised split result u_s = acc / l in fp16 (a convex combination of
-            // latent rows, so inside the fp16 range the QK operands already need)
-            const size_t slot = static_cast<size_t>(head) * p.splits + split;
-            _Float16* out = static_cast<_Float16*>(p.part_u) + slot * KL + dim0;
-            const float inv = 1.f / l[nt];
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                typedef float f32x2_t __attribute__((ext_vector_type(2)));
-                typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-                const f16x2_t lo = __builtin_convertvector(f32x2_t{acc[nt][dt][0] * inv, acc[nt][dt][1] * inv}, f16x2_t);
-                const f16x2_t hi = __builtin_convertvector(f32x2_t{acc[nt][dt][2] * inv, acc[nt][dt][3] * inv}, f16x2_t);
-                *reinterpret_cast<uint2*>(out + 16 * dt) =
-                    make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-            }
-            if (wave == 0 && q4 == 0) p.part_ml[slot] = make_float2(m[nt], l[nt]);
         }
+        return;
+    }
+    // Normalised split result u_s = acc / l in fp16 (a convex combination of latent rows,
+    // so inside the fp16 range the QK operands already need).  A lane holds 4 dims of each
+    // of 8 dim tiles of its head, so it would store 8 bytes into each of 16 head rows per
+    // instruction; the rows are assembled in LDS first (tile buffer 0, free after the
+    // barrier) and every wave store then writes one whole 1 KiB head row.
+    constexpr int SR = KL * 2 + 16;  // staged row pitch (bytes)
+    static_assert(kMHeads * SR <= TB, "staged partials must fit in one tile buffer");
+    lds_barrier();  // every wave is done with the last tile
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int hl = 16 * nt + l16;
+        const float inv = 1.f / l[nt];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            typedef float f32x2_t __attribute__((ext_vector_type(2)));
+            typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+            const f16x2_t lo = __builtin_convertvector(f32x2_t{acc[nt][dt][0] * inv, acc[nt][dt][1] * inv}, f16x2_t);
+            const f16x2_t hi = __builtin_convertvector(f32x2_t{acc[nt][dt][2] * inv, acc[nt][dt][3] * inv}, f16x2_t);
+            *reinterpret_cast<uint2*>(lds_t0 + hl * SR + 2 * (128 * wave + 16 * dt + 4 * q4)) =
+                make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+        }
+        const int head = hg * kMHeads + hl;
+        if (wave == 0 && q4 == 0 && head < p.heads)
+            p.part_ml[static_cast<size_t>(head) * p.splits + split] = make_float2(m[nt], l[nt]);
+    }
+    lds_barrier();
+    // wave w writes head rows w, w + 4, ...: lane j the 16 bytes at 16 j
+#pragma unroll
+    for (int i = 0; i < kMHeads / 4; ++i) {
+        const int hl = wave + 4 * i;
+        const int head = hg * kMHeads + hl;
+        if (head >= p.heads) break;
+        const U32x4 v = *reinterpret_cast<const U32x4*>(lds_t0 + hl * SR + 16 * lane);
+        *reinterpret_cast<U32x4*>(static_cast<char*>(p.part_u) +
+                                  (static_cast<size_t>(head) * p.splits + split) * (KL * 2) + 16 * lane) = v;
     }
 }
 
