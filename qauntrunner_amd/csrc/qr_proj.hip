@@ -152,6 +152,7 @@ struct WuvLayout {
     int slab_cols;   // columns per slab (multiple of 8 and of the block)
     int lds_stride;  // bytes per staged row (16-byte multiple, padded)
     int copy_bytes;  // 16, 4 or 2: width of the staging copies
+    int dma;         // slabs of whole 1 KiB rows, 16-byte aligned: staged by direct-to-LDS loads
     __host__ __device__ size_t tile_bytes(int nbt) const {
         return static_cast<size_t>(kWuvRows) * lds_stride + static_cast<size_t>(nbt) * slab_cols * 4;
     }
@@ -268,34 +269,74 @@ __device__ __forceinline__ void wuv_body(const MlaProjArgs& a, const WuvLayout& 
         const float* ul = reinterpret_cast<const float*>(tl + kWuvRows * L.lds_stride);
         const uint8_t* row = tl + rr * L.lds_stride;
         const int cols = min(L.slab_cols, a.kv_lora - s * L.slab_cols);
-        for (int c = 0; c < cols; c += 8 * kSteps) {
+        // whole groups of kSteps chunks: fixed offsets from the row, no clamps and no
+        // per-chunk conditions on the chains
+        int c = 0;
+        for (; c + 8 * kSteps <= cols; c += 8 * kSteps) {
             float2 w[kSteps];
 #pragma unroll
-            for (int k = 0; k < kSteps; ++k) w[k] = deq2<FMT>(row, min(c + 8 * k, cols - 8) + 2 * p);
+            for (int k = 0; k < kSteps; ++k) w[k] = deq2<FMT>(row, c + 8 * k + 2 * p);
 #pragma unroll
             for (int b = 0; b < NBT; ++b) {
                 if (b < nb) {
                     float2 uu[kSteps];
 #pragma unroll
                     for (int k = 0; k < kSteps; ++k)
-                        uu[k] = *reinterpret_cast<const float2*>(ul + b * L.slab_cols + min(c + 8 * k, cols - 8) + 2 * p);
+                        uu[k] = *reinterpret_cast<const float2*>(ul + b * L.slab_cols + c + 8 * k + 2 * p);
 #pragma unroll
                     for (int k = 0; k < kSteps; ++k) {
-                        if (c + 8 * k < cols) {
-                            acc0[b] = add_rn(acc0[b], mul_rn(w[k].x, uu[k].x));
-                            acc1[b] = add_rn(acc1[b], mul_rn(w[k].y, uu[k].y));
-                        }
+                        acc0[b] = add_rn(acc0[b], mul_rn(w[k].x, uu[k].x));
+                        acc1[b] = add_rn(acc1[b], mul_rn(w[k].y, uu[k].y));
                     }
                 }
             }
+        }
+        for (; c < cols; c += 8) {  // the last cols % (8 kSteps) columns, one chunk at a time
+            const float2 w = deq2<FMT>(row, c + 2 * p);
+#pragma unroll
+            for (int b = 0; b < NBT; ++b) {
+                if (b < nb) {
+                    const float2 uu = *reinterpret_cast<const float2*>(ul + b * L.slab_cols + c + 2 * p);
+                    acc0[b] = add_rn(acc0[b], mul_rn(w.x, uu.x));
+                    acc1[b] = add_rn(acc1[b], mul_rn(w.y, uu.y));
+                }
+            }
+        }
+    };
+
+    // Direct-to-LDS staging (1 KiB slab rows): one buffer-load DMA per weight row into its
+    // padded LDS row and one per KiB of u, split over the waves; rows past the matrix lie
+    // outside the buffer and land as zeros.  No address arithmetic or stores per copy.
+    auto dma_slab = [&](int s) {
+        const SlabGeom g = geom(s);
+        const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+        const uint32_t voff = 16u * static_cast<uint32_t>(t & 63);
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(g.src), static_cast<short>(0), nrows * static_cast<int>(a.row_bytes), kBufferFlags);
+        for (int r = wave; r < kWuvRows; r += kWuvThreads / 64)
+            buffer_load_lds16(rw, reinterpret_cast<const char*>(lds) + r * L.lds_stride, voff,
+                              static_cast<uint32_t>(r * a.row_bytes));
+        const char* ul = reinterpret_cast<const char*>(lds) + kWuvRows * L.lds_stride;
+        const int pieces = g.cols * 4 / 1024;
+#pragma unroll
+        for (int b = 0; b < NBT; ++b) {
+            const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(g.u_src + min(b, nb - 1) * u_stride), static_cast<short>(0), g.cols * 4, kBufferFlags);
+            for (int i = wave; i < pieces; i += kWuvThreads / 64)
+                buffer_load_lds16(ru, ul + b * L.slab_cols * 4 + 1024 * i, voff, static_cast<uint32_t>(1024 * i));
         }
     };
 
     SlabRegs<G, KU> R;
     for (int s = 0; s < ns; ++s) {
         if (s > 0) __syncthreads();  // the previous slab's reads are done
-        issue(R, s);
-        land(R, s);
+        if (G == 16 && L.dma) {
+            dma_slab(s);
+            wait_dma();
+        } else {
+            issue(R, s);
+            land(R, s);
+        }
         __syncthreads();
         compute(s);
     }
@@ -343,6 +384,8 @@ WuvLayout wuv_layout(const MlaProjArgs& a) {
     const uintptr_t base = reinterpret_cast<uintptr_t>(a.w);
     auto aligned = [&](int g) { return base % g == 0 && a.row_bytes % g == 0 && slab_bytes % g == 0; };
     L.copy_bytes = aligned(16) ? 16 : aligned(4) ? 4 : 2;
+    L.dma = L.copy_bytes == 16 && slab_bytes == 1024 && a.kv_lora % L.slab_cols == 0 && L.slab_cols % 256 == 0 &&
+            reinterpret_cast<uintptr_t>(a.in) % 16 == 0;
     return L;
 }
 

@@ -79,6 +79,8 @@ def test_projections_c5_shape_bf16(gpu):
     ("Q6_K", 3, 10, 8, 20, 256, 1),     # 210-byte rows (2-byte staging)
     ("Q4_K", 2, 33, 64, 64, 1024, 4),   # four super-blocks per row
     ("F16", 16, 128, 64, 128, 512, 9),  # batch of 9 queries: tiles of 4, 4, 1
+    ("BF16", 3, 36, 8, 16, 128, 2),     # nope past a whole number of 8-row DMA gathers
+    ("F16", 2, 18, 0, 8, 64, 1),        # nope not a multiple of 4: the register-block absorb
 ])
 def test_projections_ragged_shapes(gpu, fmt, heads, nope, rope, vdim, kv_lora, nq):
     qt, want_qt, out, want_out = run_proj(fmt, heads, nope, rope, vdim, kv_lora, nq, seed=nope + vdim)
