@@ -68,6 +68,17 @@ def test_matvec_ragged_shapes(gpu, fmt, rows, cols, nq):
     assert_exact(got, want, f"{fmt} {rows}x{cols} nq{nq}")
 
 
+@pytest.mark.parametrize("fmt,rows,cols,nq", [
+    ("Q4_K", 24, 32768, 1),     # 512 items a row: the padded copy of x fills 136 KiB of LDS
+    ("Q8_0", 20, 20480, 2),     # 320 block pairs: past the ring's 256, the persistent form
+    ("Q4_K", 9000, 4096, 1),    # several tiles per workgroup at two rows a thread
+])
+def test_matvec_long_rows_and_many_tiles(gpu, fmt, rows, cols, nq):
+    """Shapes whose workgroups need more than 64 KiB of LDS, or walk several row tiles."""
+    got, want, _, _ = run(fmt, rows, cols, nq, seed=rows + cols)
+    assert_exact(got, want, f"{fmt} {rows}x{cols} nq{nq}")
+
+
 def assert_exact_nan(got, want, what):
     """Bit-exact, except that any NaN matches any NaN (payloads are not compared)."""
     g, w = got.reshape(-1), want.reshape(-1)
