@@ -279,27 +279,30 @@ __device__ __forceinline__ float vecdot16_bytes(const uint32_t (&q)[4], const fl
 
 // the two terms of pair j of the block whose header is h, quants qa (bytes 32j..32j+15)
 // and qb (32j+16..32j+31), against x[0..63] and the two sub-block sums of x
+// The 6-bit scale and min of sub-block 2j+odd from the 12 scale bytes s[0..11] (h.y, h.z,
+// h.w) without a branch on j: with c = 16 (j & 1) + 8 odd, sub-blocks 0..3 (j < 2) take
+// sc = s[j2] & 63 = bits c..c+5 of h.y and m = bits c..c+5 of h.z; sub-blocks 4..7 take
+// sc = (s[8+j2] & 15) | (s[j2] >> 6) << 4 and m = (s[8+j2] >> 4) | (s[4+j2] >> 6) << 4,
+// i.e. bit fields c..c+3 / c+4..c+7 of h.w and c+6..c+7 of h.y / h.z (j2 = 2 (j & 1) + odd).
+__device__ __forceinline__ void q4k_scale_min(const u32x4_t h, int j, int odd, int& sc, int& m) {
+    const uint32_t c = 16u * static_cast<uint32_t>(j & 1) + 8u * static_cast<uint32_t>(odd);
+    const uint32_t lo_sc = __builtin_amdgcn_ubfe(h.y, c, 6), lo_m = __builtin_amdgcn_ubfe(h.z, c, 6);
+    const uint32_t hi_sc = __builtin_amdgcn_ubfe(h.w, c, 4) | (__builtin_amdgcn_ubfe(h.y, c + 6, 2) << 4);
+    const uint32_t hi_m = __builtin_amdgcn_ubfe(h.w, c + 4, 4) | (__builtin_amdgcn_ubfe(h.z, c + 6, 2) << 4);
+    sc = static_cast<int>(j >= 2 ? hi_sc : lo_sc);
+    m = static_cast<int>(j >= 2 ? hi_m : lo_m);
+}
+
 __device__ __forceinline__ void q4k_pair_terms(const u32x4_t h, const u32x4_t qa, const u32x4_t qb, int j,
                                                const float (&x)[64], float ss0, float ss1, float& t0, float& t1) {
     const float d = f16_bits_to_f32(static_cast<uint16_t>(h.x & 0xFFFFu));
     const float dmin = f16_bits_to_f32(static_cast<uint16_t>(h.x >> 16));
-    auto byte = [&](int i) {
-        const uint32_t w = i < 4 ? h.y : i < 8 ? h.z : h.w;
-        return static_cast<int>((w >> (8 * (i & 3))) & 0xFFu);
-    };
     const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w};
     const uint32_t b[4] = {qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int odd = 0; odd < 2; ++odd) {
-        const int sub = 2 * j + odd;
         int sc, m;
-        if (sub < 4) {
-            sc = byte(sub) & 63;
-            m = byte(sub + 4) & 63;
-        } else {
-            sc = (byte(sub + 4) & 0xF) | ((byte(sub - 4) >> 6) << 4);
-            m = (byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4);
-        }
+        q4k_scale_min(h, j, odd, sc, m);
         uint32_t na[4], nb[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
