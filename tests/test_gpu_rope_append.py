@@ -120,6 +120,27 @@ def test_rope_append_dev_ragged_ranges(gpu, dtype, D):
     assert np.mean(kr == enc(kw)) >= 0.99
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rope_append_dev_without_q_across_a_page(gpu, dtype):
+    """K and V only (no q rows): positions 250..286 cross the page boundary at 256 and two
+    32-position V tiles, both partial; rows before and after stay untouched."""
+    import torch
+    heads, kv_heads, D, pos0, n, theta = 8, 2, 128, 250, 37, 500000.0
+    K, V = normal(350, (n, kv_heads * D)), normal(351, (n, kv_heads * D))
+    K0, V0 = normal(352, (pos0, kv_heads * D)), normal(353, (pos0, kv_heads * D))
+    dev = torch.device("cuda")
+    with qr.PagedKvCache(1, heads, kv_heads, D, 320, kv_dtype=dtype) as kv:
+        kv.AppendRopeDev(0, 0, None, torch.from_numpy(K0).to(dev), torch.from_numpy(V0).to(dev), theta)
+        kv.AppendRopeDev(0, pos0, None, torch.from_numpy(K).to(dev), torch.from_numpy(V).to(dev), theta)
+        torch.cuda.synchronize()
+        kr, vr = kv.Read(0, 0, pos0 + n)
+        assert kv.SeqLen == pos0 + n
+    enc = oracle.f32_to_f16 if dtype == "f16" else oracle.f32_to_bf16
+    assert np.array_equal(vr, enc(np.concatenate([V0, V])))
+    kw = np.concatenate([rope_ref(K0, D, 0, theta), rope_ref(K, D, pos0, theta)])
+    assert np.mean(kr == enc(kw)) >= 0.99
+
+
 def test_rope_append_then_attention(gpu):
     """Decode over rows appended through the fused step equals the oracle's attention over
     oracle-rotated rows (fp32 accumulation tolerance)."""
