@@ -157,6 +157,14 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
  * caller can time the split-K kernel alone.  NULL turns it off. */
 int qr_kv_set_split_event(qr_kv* kv, void* event);
 
+/* Introspection, no reference counterpart: the split-K plan a decode call with
+ * these entries would take (as qr_kv_attention_batch / _dev, first 64 entries):
+ * tokens per split (a multiple of 256) and the number of splits of the longest
+ * entry (1: the split kernel writes the output, no merge).  Validates like the
+ * attention call; launches nothing. */
+int qr_kv_decode_plan(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos, int* split_tokens,
+                      int* splits);
+
 /* Reset(), PagedKvCache.cs:72 (seq_id < 0 resets every sequence). */
 int qr_kv_reset(qr_kv* kv, int seq_id);
 /* Truncate(len), PagedKvCache.cs:76: SeqLen = min(SeqLen, len). */

@@ -83,6 +83,7 @@ SIGNATURES = {
     "qr_kv_attention_chunk": [_p, _i, _i, _i, _i, _p, _i, _p, _f],
     "qr_kv_attention_chunk_dev": [_p, _i, _i, _i, _i, _p, _i, _p, _f, _p],
     "qr_kv_set_split_event": [_p, _p],
+    "qr_kv_decode_plan": [_p, _i, _p, _i, _p, _ip, _ip],
     "qr_kv_reset": [_p, _i],
     "qr_kv_truncate": [_p, _i, _i],
     "qr_kv_seq_len": [_p, _i, _ip],

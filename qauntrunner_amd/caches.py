@@ -43,6 +43,40 @@ def _dev_ptr(x):
     return ctypes.c_void_p(x.data_ptr())
 
 
+_TORCH_CODES = {"float32": 0, "float16": 1, "bfloat16": 2, "int16": -1, "uint16": -1}
+
+
+def _dev_tensor(x, numel, code, what, allow_none=False):
+    """Checks a torch tensor handed to a *Dev call before its address reaches a kernel:
+    on the GPU, contiguous, `numel` elements of the element type of dtype `code`
+    (fp32 for DTYPE_F32; 2-byte elements -- fp16, bf16 or int16/uint16 bit patterns --
+    for the 16-bit codes).  The C ABI cannot see device sizes, so a short tensor would
+    otherwise be read or written out of bounds."""
+    if x is None:
+        if allow_none:
+            return ctypes.c_void_p()
+        raise ValueError(f"{what}: tensor required")
+    if not getattr(x, "is_cuda", False):
+        raise ValueError(f"{what}: expected a tensor on the GPU")
+    if not x.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    name = str(x.dtype).replace("torch.", "")
+    tc = _TORCH_CODES.get(name)
+    ok = tc == code if code == _lib.DTYPE_F32 else tc is not None and tc != _lib.DTYPE_F32 and (tc in (-1, code))
+    if not ok:
+        raise ValueError(f"{what}: dtype {name} does not match dtype code {code}")
+    if x.numel() != numel:
+        raise ValueError(f"{what}: expected {numel} elements, got {x.numel()}")
+    return ctypes.c_void_p(x.data_ptr())
+
+
+def _rows_of(x, width, what):
+    n = x.numel() // width if x is not None else 0
+    if x is None or n * width != x.numel():
+        raise ValueError(f"{what}: element count must be a multiple of {width}")
+    return n
+
+
 def _stream_ptr(stream):
     if stream is None:
         import torch
@@ -131,10 +165,11 @@ class PagedKvCache:
         check(self._lib.qr_kv_append_range(self._h, seq_id, layer, pos0, n, _ptr(k), _ptr(v), code))
 
     def AppendRangeDev(self, layer, pos0, k_rows, v_rows, src_dtype="f32", seq_id=0, stream=None) -> None:
-        n = k_rows.numel() // self.KvDim
-        check(self._lib.qr_kv_append_range_dev(self._h, seq_id, layer, pos0, n, ctypes.c_void_p(k_rows.data_ptr()),
-                                               ctypes.c_void_p(v_rows.data_ptr()), dtype_code(src_dtype),
-                                               _stream_ptr(stream)))
+        code = dtype_code(src_dtype)
+        n = _rows_of(k_rows, self.KvDim, "k rows")
+        kp = _dev_tensor(k_rows, n * self.KvDim, code, "k rows")
+        vp = _dev_tensor(v_rows, n * self.KvDim, code, "v rows")
+        check(self._lib.qr_kv_append_range_dev(self._h, seq_id, layer, pos0, n, kp, vp, code, _stream_ptr(stream)))
 
     def AppendRope(self, layer, pos, q, k, v, theta, seq_id=0) -> np.ndarray:
         """StreamingEngine.cs:245-248: RoPE on q and k at `pos` (TransformerOps.cs:56-88),
@@ -149,10 +184,13 @@ class PagedKvCache:
 
     def AppendRopeDev(self, layer, pos0, q_rows, k_rows, v_rows, theta, seq_id=0, stream=None) -> None:
         """n positions from device rows; q_rows (or None) is rotated in place."""
-        n = k_rows.numel() // self.KvDim
-        qp = ctypes.c_void_p(q_rows.data_ptr()) if q_rows is not None else ctypes.c_void_p()
-        check(self._lib.qr_kv_append_rope_dev(self._h, seq_id, layer, pos0, n, qp, ctypes.c_void_p(k_rows.data_ptr()),
-                                              ctypes.c_void_p(v_rows.data_ptr()), theta, _stream_ptr(stream)))
+        f32 = _lib.DTYPE_F32
+        n = _rows_of(k_rows, self.KvDim, "k rows")
+        qp = _dev_tensor(q_rows, n * self.Heads * self.HeadDim, f32, "q rows", allow_none=True)
+        kp = _dev_tensor(k_rows, n * self.KvDim, f32, "k rows")
+        vp = _dev_tensor(v_rows, n * self.KvDim, f32, "v rows")
+        check(self._lib.qr_kv_append_rope_dev(self._h, seq_id, layer, pos0, n, qp, kp, vp, theta,
+                                              _stream_ptr(stream)))
 
     def Reset(self, seq_id=-1) -> None:  # PagedKvCache.cs:72
         check(self._lib.qr_kv_reset(self._h, seq_id))
@@ -184,9 +222,25 @@ class PagedKvCache:
     def AttentionDev(self, layer, seq_ids, positions, q, out, scale, stream=None) -> None:
         ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
         pos = np.ascontiguousarray(positions, dtype=np.int32)
-        check(self._lib.qr_kv_attention_dev(self._h, ids.size, _ptr(ids), layer, _ptr(pos),
-                                            ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                                            scale, _stream_ptr(stream)))
+        if pos.size != ids.size:
+            raise ValueError("seq_ids and positions must agree")
+        rows = ids.size * self.Heads * self.HeadDim
+        qp = _dev_tensor(q, rows, _lib.DTYPE_F32, "q")
+        op = _dev_tensor(out, rows, _lib.DTYPE_F32, "out")
+        check(self._lib.qr_kv_attention_dev(self._h, ids.size, _ptr(ids), layer, _ptr(pos), qp, op, scale,
+                                            _stream_ptr(stream)))
+
+    def DecodePlan(self, layer, seq_ids, positions):
+        """(tokens per split, splits of the longest entry) that a decode call with these
+        entries takes."""
+        ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        if pos.size != ids.size:
+            raise ValueError("seq_ids and positions must agree")
+        st, ns = ctypes.c_int(), ctypes.c_int()
+        check(self._lib.qr_kv_decode_plan(self._h, ids.size, _ptr(ids), layer, _ptr(pos), ctypes.byref(st),
+                                          ctypes.byref(ns)))
+        return st.value, ns.value
 
     def AttentionChunk(self, layer, pos0, q, scale, q_dtype="f32", seq_id=0) -> np.ndarray:
         """Causal attention of nq queries at pos0..pos0+nq-1 (each sees 0..its position)."""
@@ -201,9 +255,12 @@ class PagedKvCache:
         return out
 
     def AttentionChunkDev(self, layer, pos0, q, out, scale, q_dtype="f32", seq_id=0, stream=None) -> None:
-        nq = q.numel() // (self.Heads * self.HeadDim)
-        check(self._lib.qr_kv_attention_chunk_dev(self._h, seq_id, layer, pos0, nq, ctypes.c_void_p(q.data_ptr()),
-                                                  dtype_code(q_dtype), ctypes.c_void_p(out.data_ptr()), scale,
+        row = self.Heads * self.HeadDim
+        code = dtype_code(q_dtype)
+        nq = _rows_of(q, row, "q")
+        qp = _dev_tensor(q, nq * row, code, "q")
+        op = _dev_tensor(out, nq * row, _lib.DTYPE_F32, "out")
+        check(self._lib.qr_kv_attention_chunk_dev(self._h, seq_id, layer, pos0, nq, qp, code, op, scale,
                                                   _stream_ptr(stream)))
 
     # ---- debug copy-out
@@ -286,9 +343,10 @@ class MlaLatentCache:
         check(self._lib.qr_mla_append_range(self._h, layer, pos0, n, _ptr(r), code))
 
     def AppendRangeDev(self, layer, pos0, rows, src_dtype="f32", stream=None) -> None:
-        n = rows.numel() // self.LatentDim
-        check(self._lib.qr_mla_append_range_dev(self._h, layer, pos0, n, ctypes.c_void_p(rows.data_ptr()),
-                                                dtype_code(src_dtype), _stream_ptr(stream)))
+        code = dtype_code(src_dtype)
+        n = _rows_of(rows, self.LatentDim, "latent rows")
+        rp = _dev_tensor(rows, n * self.LatentDim, code, "latent rows")
+        check(self._lib.qr_mla_append_range_dev(self._h, layer, pos0, n, rp, code, _stream_ptr(stream)))
 
     def Reset(self) -> None:
         check(self._lib.qr_mla_reset(self._h))
@@ -321,13 +379,18 @@ class MlaLatentCache:
     def AttendAbsorbedDev(self, layer, pos, q, kvb, fmt, nope, vdim, out, stream=None) -> None:
         """Device form: q, out torch tensors on the GPU; kvb a Weight or a uint8 device tensor
         of rows in format `fmt`."""
-        heads = q.numel() // (nope + self.Rope)
-        check(self._lib.qr_mla_attend_absorbed_dev(self._h, layer, pos, heads, nope, vdim,
-                                                   ctypes.c_void_p(q.data_ptr()), _dev_ptr(kvb), fmt,
-                                                   ctypes.c_void_p(out.data_ptr()), _stream_ptr(stream)))
+        f32 = _lib.DTYPE_F32
+        heads = _rows_of(q, nope + self.Rope, "q")
+        qp = _dev_tensor(q, heads * (nope + self.Rope), f32, "q")
+        op = _dev_tensor(out, heads * vdim, f32, "out")
+        check(self._lib.qr_mla_attend_absorbed_dev(self._h, layer, pos, heads, nope, vdim, qp, _dev_ptr(kvb), fmt,
+                                                   op, _stream_ptr(stream)))
 
     def AbsorbedAttentionDev(self, layer, pos, q_tilde, q_rope, u, scale, stream=None) -> None:
-        heads = q_tilde.numel() // self.KvLora
-        qr_ptr = ctypes.c_void_p(q_rope.data_ptr()) if q_rope is not None else ctypes.c_void_p()
-        check(self._lib.qr_mla_attention_dev(self._h, layer, pos, heads, ctypes.c_void_p(q_tilde.data_ptr()),
-                                             qr_ptr, scale, ctypes.c_void_p(u.data_ptr()), _stream_ptr(stream)))
+        f32 = _lib.DTYPE_F32
+        heads = _rows_of(q_tilde, self.KvLora, "q_tilde")
+        qt = _dev_tensor(q_tilde, heads * self.KvLora, f32, "q_tilde")
+        qr_ptr = _dev_tensor(q_rope, heads * self.Rope, f32, "q_rope", allow_none=self.Rope == 0)
+        up = _dev_tensor(u, heads * self.KvLora, f32, "u")
+        check(self._lib.qr_mla_attention_dev(self._h, layer, pos, heads, qt, qr_ptr, scale, up,
+                                             _stream_ptr(stream)))

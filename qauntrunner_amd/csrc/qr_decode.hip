@@ -1,7 +1,8 @@
 // qr_decode.hip -- split-K (flash-decoding) GQA decode attention for gfx950.
 //
 // Replaces the two-pass, fully materialised PagedKvCache.Attention
-// (PagedKvCache.cs:83-136) with decode_stream_kernel + decode_combine_kernel.
+// (PagedKvCache.cs:83-136) with decode_stream_kernel (decode_mfma_kernel for
+// 16-bit caches) + decode_combine_kernel.
 //
 // Grid: (split, unit, entry).  A unit is one kv head with up to GMAX of its
 // query heads (or one query head when kv_heads does not divide heads).  A
@@ -30,6 +31,7 @@
 // decode_combine_kernel then merges the splits of every (entry, head); an
 // entry covered by a single split is written directly by the split kernel.
 #include "qr_kernels.hpp"
+#include "qr_mfma.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -41,8 +43,13 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kPrefetch = 2;        // steps in flight beyond the one being computed (3 buffers)
-constexpr int kMaxSplits = 256;     // splits per (entry, unit) merged by the last workgroup
+// Register buffers of the step pipeline: one step in flight beyond the one computed.
+// Measured at the 8B 32K fp32 shape: 2 buffers 52.0-52.3 us per call, 3 buffers
+// 53.0-53.4, 4-6 buffers slower still (the loads queue deeper in the memory system
+// without moving more bytes).
+constexpr int kStreamBuffers = 2;
+constexpr int kPrefetch = kStreamBuffers - 1;
+constexpr int kMaxSplits = 256;     // splits per entry (grid x dimension of a launch)
 constexpr int kMaxGroup = 8;        // GMAX upper bound
 
 struct DecodeK {
@@ -60,8 +67,9 @@ struct DecodeK {
     int units;
     const float* q;
     float* out;
-    float* part_acc;     // [nb][heads][kMaxSplits][head_dim]
-    float2* part_ml;     // [nb][heads][kMaxSplits] (max in log2 units, sum)
+    float* part_acc;     // [nb][heads][split_stride][head_dim]
+    float2* part_ml;     // [nb][heads][split_stride] (max in log2 units, sum)
+    int split_stride;    // splits of the longest entry
     float qscale;        // scale * log2(e)
     int split_tokens;
     int seq_len[kMaxDecodeBatch];
@@ -70,16 +78,6 @@ struct DecodeK {
 
 __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
-}
-
-typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 mfma_f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 mfma_bf16x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ mfma_f32x4 mfma16(mfma_f16x8 a, mfma_f16x8 b, mfma_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ mfma_f32x4 mfma16(mfma_bf16x8 a, mfma_bf16x8 b, mfma_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // DT: head_dim fixed at compile time (0: read from the arguments).
@@ -128,26 +126,41 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     const int row_in_step = tg;  // + u * ntg
     const int nsteps = (t_end - t_begin + step_tokens - 1) / step_tokens;
 
-    // chunk c of the K (plane 0) or V (plane 1) row `slot` of physical page `phys`
-    auto row_ptr = [&](long long phys, int plane, int slot) -> const char* {
-        return p.pool + (phys * p.page_elems + plane * p.plane_elems + head_off +
-                         static_cast<long long>(slot) * D) * ESZ;
-    };
+    // Addresses are a wave-uniform 64-bit base (the step's first row in the (page, kv
+    // head) block, in SGPRs) plus a loop-invariant 32-bit lane offset, so the loads take
+    // the scalar-base form and no per-lane address is recomputed per step.  (With
+    // per-lane 64-bit addresses the compiler rebuilt them every step in registers that
+    // the previous step's loads were still writing, and waited for every load in
+    // flight -- the whole prefetch -- once per loop iteration.)
+    const uint32_t lane_off = static_cast<uint32_t>((row_in_step * D + sub * EPC) * ESZ);
 
     U32x4 kbuf[kPrefetch + 1][UMAX][NC];
     U32x4 vbuf[kPrefetch + 1][UMAX][NC];
+    // Splits start at different steps and wrap around: in lockstep, every workgroup
+    // would read the same offset of its page at the same moment (measured: 1.5-3 us per
+    // 32K-token call).  The units of one split stay together (rotating them apart too
+    // cost 5% at batch 16).
+    const int rot = (split * 7) % nsteps;
+    auto step_t0 = [&](int st) { return t_begin + (st + rot < nsteps ? st + rot : st + rot - nsteps) * step_tokens; };
     auto issue = [&](int st, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
-        const int t0 = t_begin + st * step_tokens;       // uniform: a step never crosses a page
+        const int t0 = step_t0(st);  // uniform: a step never crosses a page
         const long long phys = pt[t0 >> kPageShift];
-        const int slot0 = (t0 & (kPageTokens - 1)) + row_in_step;
+        const char* kbase = p.pool + (phys * p.page_elems + head_off +
+                                      static_cast<long long>(t0 & (kPageTokens - 1)) * D) * ESZ;
+        // one buffer resource over the step's K rows and V rows (both planes of the page):
+        // the byte offsets of the step stay far below 2^32
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(kbase), 0, 0x7FFFFFFF, kBufferFlags);
+        const uint32_t vplane = static_cast<uint32_t>(p.plane_elems * ESZ);
 #pragma unroll
         for (int u = 0; u < UMAX; ++u) {
-            const char* kr = row_ptr(phys, 0, slot0 + u * ntg);
-            const char* vr = row_ptr(phys, 1, slot0 + u * ntg);
+            const uint32_t off = lane_off + static_cast<uint32_t>(u * ntg * D * ESZ);
 #pragma unroll
-            for (int j = 0; j < NC; ++j) kb[u][j] = load16(kr + (sub + LPT * j) * 16);
+            for (int j = 0; j < NC; ++j)
+                kb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + LPT * j * 16, 0, 0));
 #pragma unroll
-            for (int j = 0; j < NC; ++j) vb[u][j] = load16(vr + (sub + LPT * j) * 16);
+            for (int j = 0; j < NC; ++j)
+                vb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + LPT * j * 16, vplane, 0));
         }
     };
 
@@ -161,7 +174,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     }
 
     auto compute = [&](int st, const U32x4 (&kb)[UMAX][NC], const U32x4 (&vb)[UMAX][NC]) {
-        const int t0 = t_begin + st * step_tokens + row_in_step;
+        const int t0 = step_t0(st) + row_in_step;
         float s[UMAX][GMAX];
 #pragma unroll
         for (int u = 0; u < UMAX; ++u) {
@@ -235,18 +248,26 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
                 q[g][j * EPC + e] = qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f);
             }
 
-    issue(min(1, nsteps - 1), kbuf[1], vbuf[1]);
-    for (int s0 = 0;; s0 += 3) {  // exits only through the breaks: the back-edge is steady state
-        issue(s0 + 2 < nsteps ? s0 + 2 : s0, kbuf[2], vbuf[2]);
-        compute(s0, kbuf[0], vbuf[0]);
-        if (s0 + 1 >= nsteps) break;
-        issue(s0 + 3 < nsteps ? s0 + 3 : s0 + 1, kbuf[0], vbuf[0]);
-        compute(s0 + 1, kbuf[1], vbuf[1]);
-        if (s0 + 2 >= nsteps) break;
-        issue(s0 + 4 < nsteps ? s0 + 4 : s0 + 2, kbuf[1], vbuf[1]);
-        compute(s0 + 2, kbuf[2], vbuf[2]);
-        if (s0 + 3 >= nsteps) break;
+#pragma unroll
+    for (int i = 1; i < kPrefetch; ++i) issue(min(i, nsteps - 1), kbuf[i], vbuf[i]);
+    // Unrolled by the buffer count so every buffer index is a constant: step s0 + k is
+    // computed from buffer k while step s0 + k + kPrefetch is loaded into the buffer
+    // computed last (past the end, the step being computed is loaded again).  Exits only
+    // through the goto: the back-edge is steady state.
+    for (int s0 = 0;; s0 += kStreamBuffers) {
+#pragma unroll
+        for (int k = 0; k < kStreamBuffers; ++k) {
+            const int ahead = s0 + k + kPrefetch;
+            issue(ahead < nsteps ? ahead : s0 + k, kbuf[(k + kPrefetch) % kStreamBuffers],
+                  vbuf[(k + kPrefetch) % kStreamBuffers]);
+            // the loads leave before any use of the step being computed, so that waiting
+            // for that step never holds back the next one
+            __builtin_amdgcn_sched_barrier(0);
+            compute(s0 + k, kbuf[k], vbuf[k]);
+            if (s0 + k + 1 >= nsteps) goto streamed;
+        }
     }
+streamed:
 
     // ---- merge the token groups of the wave (lanes with equal `sub`)
     for (int off = LPT; off < 64; off <<= 1) {
@@ -302,7 +323,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
         if (nsplit == 1) {
             p.out[(row_base + h) * D + d] = o / L;
         } else {
-            const size_t slot = (row_base + h) * kMaxSplits + split;
+            const size_t slot = (row_base + h) * p.split_stride + split;
             p.part_acc[slot * D + d] = o;
             if (d == 0) p.part_ml[slot] = make_float2(M, L);
         }
@@ -379,12 +400,15 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     const int krow = 8 * (n >> 2) + (n & 3);  // QK row of this lane in M tile 0 (+4 in tile 1)
     const int total_steps = (t_end - t_begin + kStep - 1) / kStep;
     const int nst = total_steps > wave ? (total_steps - wave + kWaves - 1) / kWaves : 0;
+    // splits start at different steps and wrap around (see decode_stream_kernel)
+    const int rot = (split * 7) % total_steps;
+    auto step_t0 = [&](int st) { return t_begin + (st + rot < total_steps ? st + rot : st + rot - total_steps) * kStep; };
 
     constexpr int NB = kMfmaBuffers;
     U32x4 kb[NB][2][NK];
     U32x4 vb[NB][NDT];
     auto issue = [&](int st, int buf) {
-        const int t0 = t_begin + st * kStep;  // a step never crosses a page
+        const int t0 = step_t0(st);  // a step never crosses a page
         const long long phys = pt[t0 >> kPageShift];
         const int slot0 = t0 & (kPageTokens - 1);
         const char* kp = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
@@ -436,7 +460,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     float m = -INFINITY, l = 0.f;
 
     auto compute = [&](int st, int buf) {
-        const int t0 = t_begin + st * kStep;
+        const int t0 = step_t0(st);
         f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
@@ -556,7 +580,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         if (nsplit == 1) {
             p.out[(row_base + h) * D + d] = o / L;
         } else {
-            const size_t slot = (row_base + h) * kMaxSplits + split;
+            const size_t slot = (row_base + h) * p.split_stride + split;
             p.part_acc[slot * D + d] = o;
             if (d == 0) p.part_ml[slot] = make_float2(M, L);
         }
@@ -575,7 +599,7 @@ __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK 
     const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
     if (nsplit <= 1) return;
     const int D = p.head_dim;
-    const size_t base = (static_cast<size_t>(b) * p.heads + h) * kMaxSplits;
+    const size_t base = (static_cast<size_t>(b) * p.heads + h) * p.split_stride;
     const int d4n = D >> 2;
     const int groups = kThreads / d4n;
     const int d4 = threadIdx.x % d4n;
@@ -761,7 +785,7 @@ DecodePlan plan_decode(const DecodeArgs& a) {
     pl.split_tokens = static_cast<int>(pps) * kPageTokens;
     pl.max_splits = (max_pages + static_cast<int>(pps) - 1) / static_cast<int>(pps);
     pl.workspace_bytes = pl.max_splits > 1
-        ? static_cast<size_t>(a.nb) * a.heads * kMaxSplits * (static_cast<size_t>(a.geom.head_dim) * 4 + 8)
+        ? static_cast<size_t>(a.nb) * a.heads * pl.max_splits * (static_cast<size_t>(a.geom.head_dim) * 4 + 8)
         : 0;
     return pl;
 }
@@ -790,9 +814,10 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
     }
     k.q = a.q;
     k.out = a.out;
-    const size_t slots = static_cast<size_t>(a.nb) * a.heads * kMaxSplits;
+    const size_t slots = static_cast<size_t>(a.nb) * a.heads * pl.max_splits;
     k.part_acc = static_cast<float*>(workspace);
     k.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + slots * a.geom.head_dim * 4);
+    k.split_stride = pl.max_splits;
     k.qscale = static_cast<float>(static_cast<double>(a.scale) * 1.4426950408889634);
     k.split_tokens = pl.split_tokens;
     for (int i = 0; i < a.nb; ++i) {

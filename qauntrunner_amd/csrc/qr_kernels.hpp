@@ -103,7 +103,7 @@ struct DecodePlan {
     int split_tokens;  // tokens per workgroup
     int max_splits;    // splits of the longest entry
     int units;         // workgroups per (entry, split): kv heads x head chunks, or heads
-    size_t workspace_bytes;
+    size_t workspace_bytes;  // split partials
 };
 DecodePlan plan_decode(const DecodeArgs& a);
 // workspace: at least plan.workspace_bytes of device memory (split partials).

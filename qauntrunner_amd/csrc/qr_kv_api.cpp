@@ -403,11 +403,6 @@ int chunk_common(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void*
         qsrc = st;
     }
     float* q32 = reinterpret_cast<float*>(st + ((qbytes + 255) & ~size_t(255)));
-    const float* qf = static_cast<const float*>(qsrc);
-    if (q_dtype != QR_DTYPE_F32) {
-        QR_HIP(launch_widen(qsrc, q_dtype, q32, static_cast<long long>(nq) * rowf, stream));
-        qf = q32;
-    }
     float* dout = out_is_dev ? attn : q32 + nq * rowf;
     if (chunk_mfma_eligible(kv->dtype, kv->head_dim, kv->heads, kv->kv_heads)) {
         // MFMA tiles read each K/V tile once for a block of queries
@@ -427,7 +422,14 @@ int chunk_common(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void*
         QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
         QR_HIP(launch_chunk(c, plan, kv->workspace.get(), stream, kv->split_event));
     } else {
-        // exact fp32 path: every query is one decode entry with its causal length
+        // exact fp32 path: every query is one decode entry with its causal length; the
+        // decode kernels read fp32 queries, so 16-bit ones are widened first (the MFMA
+        // branch above reads them in their own type)
+        const float* qf = static_cast<const float*>(qsrc);
+        if (q_dtype != QR_DTYPE_F32) {
+            QR_HIP(launch_widen(qsrc, q_dtype, q32, static_cast<long long>(nq) * rowf, stream));
+            qf = q32;
+        }
         std::vector<int> ids(nq, seq_id), lens(nq);
         for (int i = 0; i < nq; ++i) lens[i] = pos0 + i + 1;
         QR_TRY(decode_dev(kv, nq, ids.data(), lens.data(), layer, qf, dout, scale, stream));
@@ -453,6 +455,26 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
     QR_TRY(check_handle(kv));
     return chunk_common(kv, seq_id, layer, pos0, nq, q_dev, q_dtype, attn_dev, true, true, scale,
                         as_stream(stream));
+}
+
+int qr_kv_decode_plan(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos, int* split_tokens,
+                      int* splits) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(split_tokens && splits, "null output pointer");
+    std::vector<int> seq_len;
+    QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
+    DeviceGuard dg(kv->device);
+    DecodeArgs a{};
+    a.geom = kv->store.geom();
+    a.dtype = kv->dtype;
+    a.heads = kv->heads;
+    a.nb = std::min(n, kMaxDecodeBatch);
+    for (int i = 0; i < a.nb; ++i) a.seq_len[i] = seq_len[i];
+    const DecodePlan plan = plan_decode(a);
+    *split_tokens = plan.split_tokens;
+    *splits = plan.max_splits;
+    return QR_OK;
 }
 
 int qr_kv_set_split_event(qr_kv* kv, void* event) {

@@ -37,11 +37,14 @@ __device__ __forceinline__ void lds_barrier_dma_in_flight() {
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding: vmcnt bits
-// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).  The empty asm with a memory clobber keeps
+// the compiler from moving LDS reads of DMA-written data above the wait (the waitcnt
+// builtin itself is not a memory operation for the optimiser).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+    asm volatile("" ::: "memory");
 }
 // this wave's LDS-DMA writes have all landed
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
@@ -49,16 +52,14 @@ __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 
 // 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
-// ... lds); out-of-range offsets read zeros.  Inline asm, so that the compiler, which
-// cannot tell the LDS range a DMA writes, does not insert waits for it before
-// unrelated LDS reads; completion is awaited explicitly (wait_vmcnt) before the data
-// is read.
+// ... lds); out-of-range offsets read zeros.  `lds` must be the same for every lane of
+// the wave (it becomes M0, which the compiler sets).  The compiler does not track when
+// an LDS DMA lands, so completion is awaited explicitly (wait_vmcnt, then a barrier when
+// other waves read the data) before the data is read.
 __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, const char* lds, uint32_t voffset,
                                                   uint32_t soffset) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)lds)));
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset) : "memory", "m0");
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (__attribute__((address_space(3))) void*)(const_cast<char*>(lds)), 16, voffset, soffset, 0, 0);
 }
 
 }  // namespace qr

@@ -27,7 +27,7 @@ void clear_error() { g_last_error.clear(); }
 const char* last_error() { return g_last_error.c_str(); }
 
 // ---------------------------------------------------------------- DevBuf
-int DevBuf::ensure(size_t bytes) {
+int DevBuf::ensure(size_t bytes, bool zero) {
     if (bytes <= size_) return QR_OK;
     if (ptr_) {
         QR_HIP(hipDeviceSynchronize());
@@ -39,6 +39,7 @@ int DevBuf::ensure(size_t bytes) {
     want = (want + 255) & ~static_cast<size_t>(255);
     QR_HIP(hipMalloc(&ptr_, want));
     size_ = want;
+    if (zero) QR_HIP(hipMemset(ptr_, 0, want));
     return QR_OK;
 }
 

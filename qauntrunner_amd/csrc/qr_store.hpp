@@ -30,7 +30,8 @@ private:
 class DevBuf {
 public:
     ~DevBuf() { if (ptr_) (void)hipFree(ptr_); }
-    int ensure(size_t bytes);
+    // zero: a new allocation is zero-filled before it is returned
+    int ensure(size_t bytes, bool zero = false);
     void* get() const { return ptr_; }
     size_t size() const { return size_; }
 

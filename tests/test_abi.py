@@ -98,3 +98,37 @@ def test_projection_arguments_validate_before_device():
     assert L.qr_mla_attend_absorbed(null, 0, 0, 8, 128, 128, fake, fake, fake) == _lib.QR_ERR_INVALID_ARGUMENT
     h = ctypes.c_void_p()
     assert L.qr_weight_create(ctypes.byref(h), 4, 4, 48, fake) == _lib.QR_ERR_INVALID_ARGUMENT and not h.value
+
+
+class _FakeTensor:
+    """Just enough of a torch tensor for the device-argument checks."""
+
+    def __init__(self, numel, dtype="torch.float32", cuda=True, contiguous=True):
+        self._n, self.dtype, self.is_cuda, self._c = numel, dtype, cuda, contiguous
+
+    def numel(self):
+        return self._n
+
+    def is_contiguous(self):
+        return self._c
+
+    def data_ptr(self):
+        return 0x1000
+
+
+def test_device_tensor_arguments_are_checked_on_the_host():
+    from qauntrunner_amd.caches import _dev_tensor
+
+    assert _dev_tensor(_FakeTensor(8), 8, _lib.DTYPE_F32, "q").value == 0x1000
+    assert _dev_tensor(_FakeTensor(8, "torch.int16"), 8, _lib.DTYPE_F16, "k").value == 0x1000
+    assert _dev_tensor(_FakeTensor(8, "torch.bfloat16"), 8, _lib.DTYPE_BF16, "k").value == 0x1000
+    assert _dev_tensor(None, 8, _lib.DTYPE_F32, "q_rope", allow_none=True).value is None
+    for t, code in ((_FakeTensor(7), _lib.DTYPE_F32),                       # short
+                    (_FakeTensor(8, cuda=False), _lib.DTYPE_F32),           # host tensor
+                    (_FakeTensor(8, contiguous=False), _lib.DTYPE_F32),     # strided view
+                    (_FakeTensor(8, "torch.float16"), _lib.DTYPE_F32),      # wrong element type
+                    (_FakeTensor(8, "torch.float16"), _lib.DTYPE_BF16),
+                    (_FakeTensor(8), _lib.DTYPE_F16),
+                    (None, _lib.DTYPE_F32)):
+        with pytest.raises(ValueError):
+            _dev_tensor(t, 8, code, "x")

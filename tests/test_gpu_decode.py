@@ -336,3 +336,104 @@ def test_c4_llama70b_decode_128k_fp16(gpu):
         got = kv.Attention(0, n - 1, q, 1 / math.sqrt(D))
     check_decode(got, K.astype(np.float32), V.astype(np.float32), q, heads, kv_heads, D, 1 / math.sqrt(D),
                  "C4 decode f16")
+
+
+def test_c2_llama8b_decode_32k_batch16_fp32(gpu):
+    """Batch 16 of 32,768 fp32 tokens each, pages of the 16 sequences interleaved in the pool.
+    This batch takes the plan of 16 pages per split (8 splits per entry), the longest split
+    plan of the streaming kernel; single-sequence calls take 4 pages per split."""
+    import torch
+
+    heads, kv_heads, D, n, B = 32, 8, 128, 32768, 16
+    kv_dim, chunk, scale = kv_heads * D, 4096, 1 / math.sqrt(D)
+    checked = (0, 7, 15)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(600)
+    host = {b: ([], []) for b in checked}
+    with qr.PagedKvCache(1, heads, kv_heads, D, n, kv_dtype="f32", max_batch=B) as kv:
+        kv.Reserve(B * 128)
+        for p0 in range(0, n, chunk):  # interleave so page tables are not contiguous runs
+            for b in range(B):
+                K = torch.randn(chunk, kv_dim, device=gpu, generator=g)
+                V = torch.randn(chunk, kv_dim, device=gpu, generator=g)
+                kv.AppendRangeDev(0, p0, K, V, seq_id=b)
+                if b in host:
+                    host[b][0].append(K.cpu().numpy())
+                    host[b][1].append(V.cpu().numpy())
+        torch.cuda.synchronize()
+        assert kv.BytesUsed == B * 128 * 256 * kv_dim * 4 * 2
+        ids, pos = list(range(B)), [n - 1] * B
+        assert kv.DecodePlan(0, ids, pos) == (16 * 256, 8)
+        q = normal(601, (B, heads * D))
+        out = kv.AttentionBatch(0, ids, pos, q, scale)
+        for b in checked:
+            K, V = np.concatenate(host[b][0]), np.concatenate(host[b][1])
+            check_decode(out[b], K, V, q[b], heads, kv_heads, D, scale, f"C2 f32 B16 entry {b}")
+        assert kv.DecodePlan(0, [7], [n - 1]) == (4 * 256, 32)
+        assert_close(kv.Attention(0, n - 1, q[7], scale, seq_id=7), out[7], 1e-6, 1e-5, "B16 entry 7 vs single")
+        # the device entry point gives the batch call's result
+        qd = torch.from_numpy(q).to(gpu)
+        od = torch.empty_like(qd)
+        kv.AttentionDev(0, ids, pos, qd, od, scale)
+        torch.cuda.synchronize()
+        assert np.array_equal(od.cpu().numpy(), out)
+
+
+@pytest.mark.parametrize("D,heads,kv_heads", [(16, 64, 32), (32, 32, 32)])
+def test_decode_fp32_sixteen_page_splits(gpu, D, heads, kv_heads):
+    """Small kv rows and a batch large enough that the plan takes 16 pages per split, with a
+    ragged last split (one entry ends inside a page, one spans fewer pages than a split)."""
+    lens = [10240, 9000, 5000, 10240]
+    B, kv_dim, scale = len(lens), kv_heads * D, 1 / math.sqrt(D)
+    data = [(normal(700 + 2 * b, (n, kv_dim)), normal(701 + 2 * b, (n, kv_dim))) for b, n in enumerate(lens)]
+    with qr.PagedKvCache(1, heads, kv_heads, D, max(lens), max_batch=B) as kv:
+        for p0 in range(0, max(lens), 2048):
+            for b, n in enumerate(lens):
+                if p0 < n:
+                    e = min(n, p0 + 2048)
+                    kv.AppendRange(0, p0, data[b][0][p0:e], data[b][1][p0:e], seq_id=b)
+        ids, pos = list(range(B)), [n - 1 for n in lens]
+        assert kv.DecodePlan(0, ids, pos) == (16 * 256, 3)
+        q = normal(710, (B, heads * D))
+        out = kv.AttentionBatch(0, ids, pos, q, scale)
+        for b, n in enumerate(lens):
+            check_decode(out[b], data[b][0], data[b][1], q[b], heads, kv_heads, D, scale,
+                         f"16-page splits D{D} entry {b} ({n} tokens)")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_split_merge_over_many_back_to_back_calls(gpu, dtype):
+    """The last split workgroup of each (entry, unit) merges the unit's splits inside the
+    kernel, reading partials written by workgroups on other XCDs.  Many calls queued back
+    to back on one handle (alternating layers and batch sizes, new queries each time, no
+    host synchronisation between them) must each match the oracle: a stale partial or a
+    counter left non-zero by an earlier call would show up as a mismatch."""
+    import torch
+
+    heads, kv_heads, D, n = 32, 8, 128, 8192
+    scale = 1 / math.sqrt(D)
+    data = []
+    with qr.PagedKvCache(2, heads, kv_heads, D, n, kv_dtype=dtype, max_batch=3) as kv:
+        for layer in range(2):
+            for s in range(3):
+                Kb, Kd = to_dtype_bits(normal(800 + 10 * layer + s, (n, kv_heads * D)), dtype)
+                Vb, Vd = to_dtype_bits(normal(850 + 10 * layer + s, (n, kv_heads * D)), dtype)
+                kv.AppendRange(layer, 0, Kb, Vb, src_dtype=dtype, seq_id=s)
+                data.append((Kd, Vd))
+        calls = []
+        for i in range(48):
+            layer, nb = i % 2, 1 + i % 3
+            pos = [n - 1 - 37 * ((i + s) % 5) for s in range(nb)]
+            q = torch.from_numpy(normal(900 + i, (nb, heads * D))).to(gpu)
+            out = torch.empty_like(q)
+            kv.AttentionDev(layer, list(range(nb)), pos, q, out, scale)
+            calls.append((layer, pos, q, out))
+        torch.cuda.synchronize()
+        for i, (layer, pos, q, out) in enumerate(calls):
+            got, qh = out.cpu().numpy(), q.cpu().numpy()
+            for s, p in enumerate(pos):
+                if (i + s) % 4:  # a sample of the entries against the oracle
+                    continue
+                K, V = data[3 * layer + s]
+                assert_close(got[s], oracle_decode(K[:p + 1], V[:p + 1], qh[s], heads, kv_heads, D, scale),
+                             TOL_ABS, TOL_REL, f"{dtype} call {i} entry {s}")
