@@ -139,6 +139,19 @@ int qr_kv_attention_batch(qr_kv* kv, int n, const int* seq_ids, int layer, const
 int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
                         const float* q_dev, float* attn_dev, float scale, void* stream);
 
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same as qr_kv_attention_dev, but the split partials live in a
+ * fixed 8 MiB device array of the library (one per GPU, held until the process
+ * ends) instead of the handle's workspace, which grows with hipMalloc; nothing is
+ * allocated, on the host or the device.  At most 64 entries per call; a call whose
+ * split partials (entries x heads x splits x (head_dim x 4 + 8) bytes) exceed
+ * 8 MiB returns QR_ERR_OUT_OF_RANGE.  Every call on a GPU shares that GPU's array,
+ * whatever the handle: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. */
+int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
+                                const float* q_dev, float* attn_dev, float scale, void* stream);
+
 /* Causal multi-query attention over one sequence: query i sits at position
  * pos0+i and attends positions 0..pos0+i.  This is what nq sequential
  * Attention calls with interleaved appends compute (chunked prompt

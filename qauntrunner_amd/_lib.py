@@ -80,6 +80,7 @@ SIGNATURES = {
     "qr_kv_attention": [_p, _i, _i, _i, _p, _p, _f],
     "qr_kv_attention_batch": [_p, _i, _p, _i, _p, _p, _p, _f],
     "qr_kv_attention_dev": [_p, _i, _p, _i, _p, _p, _p, _f, _p],
+    "qr_kv_attention_dev_noalloc": [_p, _i, _p, _i, _p, _p, _p, _f, _p],
     "qr_kv_attention_chunk": [_p, _i, _i, _i, _i, _p, _i, _p, _f],
     "qr_kv_attention_chunk_dev": [_p, _i, _i, _i, _i, _p, _i, _p, _f, _p],
     "qr_kv_set_split_event": [_p, _p],

@@ -230,6 +230,19 @@ class PagedKvCache:
         check(self._lib.qr_kv_attention_dev(self._h, ids.size, _ptr(ids), layer, _ptr(pos), qp, op, scale,
                                             _stream_ptr(stream)))
 
+    def AttentionDevNoAlloc(self, layer, seq_ids, positions, q, out, scale, stream=None) -> None:
+        """AttentionDev through qr_kv_attention_dev_noalloc: split partials in the library's
+        fixed device array, no allocation (at most 64 entries, 8 MiB of partials)."""
+        ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        if pos.size != ids.size:
+            raise ValueError("seq_ids and positions must agree")
+        rows = ids.size * self.Heads * self.HeadDim
+        qp = _dev_tensor(q, rows, _lib.DTYPE_F32, "q")
+        op = _dev_tensor(out, rows, _lib.DTYPE_F32, "out")
+        check(self._lib.qr_kv_attention_dev_noalloc(self._h, ids.size, _ptr(ids), layer, _ptr(pos), qp, op, scale,
+                                                    _stream_ptr(stream)))
+
     def DecodePlan(self, layer, seq_ids, positions):
         """(tokens per split, splits of the longest entry) that a decode call with these
         entries takes."""

@@ -763,6 +763,40 @@ int units_of(const DecodeArgs& a, int* gmax) {
 
 }  // namespace
 
+// Split partials of qr_kv_attention_dev_noalloc: a fixed array in device memory, so the
+// call allocates nothing.  Each GPU holds its own copy until the process ends; in host
+// code the array's name is not a device address, so its address is taken once per
+// device with hipGetSymbolAddress and only that address is used.
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+int decode_scratch_address(int device, void** ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) {
+        set_error("device %d outside [0, %d)", device, kMaxDevices);
+        return QR_ERR_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        int cur = -1;
+        QR_HIP(hipGetDevice(&cur));
+        if (cur != device) {
+            set_error("scratch address requested for device %d while device %d is current", device, cur);
+            return QR_ERR_INVALID_ARGUMENT;
+        }
+        void* a = nullptr;
+        QR_HIP(hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)));
+        if (!a) {
+            set_error("hipGetSymbolAddress returned a null scratch address on device %d", device);
+            return QR_ERR_HIP;
+        }
+        addr[device] = a;
+    }
+    *ptr = addr[device];
+    return QR_OK;
+}
+
 DecodePlan plan_decode(const DecodeArgs& a) {
     DecodePlan pl{};
     int gmax = 1;

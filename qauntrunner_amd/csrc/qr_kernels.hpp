@@ -112,4 +112,11 @@ DecodePlan plan_decode(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, void* workspace, hipStream_t stream,
                          hipEvent_t after_split = nullptr);
 
+// Split partials of the no-allocation decode entry point: a device array of this many
+// bytes (per GPU, for the life of the process).
+constexpr size_t kDecodeScratchBytes = size_t(8) << 20;
+// Device address of that array on `device`, which must be the current device; taken
+// once per device with hipGetSymbolAddress (thread-safe).
+int decode_scratch_address(int device, void** ptr);
+
 }  // namespace qr

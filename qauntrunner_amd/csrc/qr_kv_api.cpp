@@ -24,6 +24,7 @@ struct qr_kv {
     DevBuf stage;      // host <-> device staging of rows, queries and outputs
     DevBuf workspace;  // split-K partials
     hipEvent_t split_event = nullptr;  // benchmark instrumentation (qr_kv_set_split_event)
+    void* scratch = nullptr;           // this device's decode scratch array (no-allocation calls)
 };
 
 namespace {
@@ -214,6 +215,7 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
         g.v_dims_major = kv_v_dims_major(kv_dtype, head_dim) ? 1 : 0;
         st = kv->store.init(g, kv_dtype, layers, max_batch, max_seq);
     }
+    if (st == QR_OK) st = decode_scratch_address(kv->device, &kv->scratch);
     if (st == QR_OK && hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed");
         st = QR_ERR_HIP;
@@ -377,6 +379,43 @@ int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const i
     QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
     DeviceGuard dg(kv->device);
     return decode_dev(kv, n, seq_ids, seq_len.data(), layer, q_dev, attn_dev, scale, as_stream(stream));
+}
+
+int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
+                                const float* q_dev, float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
+    QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for the no-allocation call", n,
+                 kMaxDecodeBatch);
+    QR_CHECK_ARG(seq_ids && pos, "null seq_ids/pos array");
+    DecodeArgs a{};  // fixed-size descriptor: no host or device allocation on this path
+    for (int i = 0; i < n; ++i) {
+        QR_TRY(check_seq_layer(kv, seq_ids[i], layer));
+        QR_TRY(check_pos(kv, pos[i]));
+        QR_TRY(check_resident(kv, seq_ids[i], layer, pos[i]));
+        a.seq_len[i] = pos[i] + 1;
+        a.pt_off[i] = kv->store.pt_offset(seq_ids[i], layer);
+    }
+    DeviceGuard dg(kv->device);
+    a.pool = kv->store.pool();
+    a.page_table = kv->store.page_table_dev();
+    a.geom = kv->store.geom();
+    a.dtype = kv->dtype;
+    a.heads = kv->heads;
+    a.q = q_dev;
+    a.out = attn_dev;
+    a.scale = scale;
+    a.nb = n;
+    const DecodePlan plan = plan_decode(a);
+    if (plan.workspace_bytes > kDecodeScratchBytes) {
+        set_error("split partials of %zu bytes exceed the %zu-byte scratch of the no-allocation call "
+                  "(fewer entries or shorter sequences per call, or qr_kv_attention_dev)",
+                  plan.workspace_bytes, kDecodeScratchBytes);
+        return QR_ERR_OUT_OF_RANGE;
+    }
+    QR_HIP(launch_decode(a, plan, kv->scratch, as_stream(stream), kv->split_event));
+    return QR_OK;
 }
 
 namespace {
