@@ -148,9 +148,10 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // of 64 positions.  A tile (64 latent rows, contiguous inside one page) is copied
 // into LDS by the LDS-DMA path (global_load_lds_dwordx4), into one of two
 // buffers, so the copy of tile t+1 runs under the MFMAs of tile t.
-//   QK  wave w scores positions 16w..16w+15 of the tile for all 32 heads:
-//       S^T[pos][head] = C[pos][dims] . q~^T[dims][head]; A is read from the
-//       row-major tile, B = q~ (fp16) stays in registers.
+//   QK  wave w scores positions 32(w/2)..32(w/2)+31 of the tile for heads
+//       16(w%2)..16(w%2)+15: S^T[pos][head] = C[pos][dims] . q~^T[dims][head]; A is
+//       read from the row-major tile, B = the wave's 16 heads of q~ (hi + lo) stays in
+//       registers.
 //   The scores go through LDS so that every wave sees all 64 positions; every
 //   wave runs the same online softmax (log2 units) and so holds the same (m, l).
 //   PV  wave w owns latent dims 128w..128w+127 for all 32 heads:
@@ -164,12 +165,16 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 //   element j%4 of them.
 // In PV the 8 k-slots of lane quarter q are the positions {4q..4q+3, 16+4q..16+4q+3}
 // of a 32-position step, so each half of a transposed read touches 8 distinct rows.
-// QK runs in fp16 for both cache types: q~ keeps 11 mantissa bits (bf16's 8 would
-// dominate the error), bf16 latent elements are converted when read from LDS
-// (exact for |x| in the fp16 normal range).  q~ is pre-multiplied per head by the
-// power of two that brings its largest element to at most 2^14 (exact) and the
-// scores are scaled back, so q~ never overflows fp16.  PV runs in the cache's type:
-// the latent is used unconverted and P (in [0, 1]) is rounded to fp16 or bf16.
+// Both products run in the cache's own 16-bit type, so the latent enters every MFMA
+// unconverted and any finite latent value is handled exactly.  QK: q~ is split into
+// hi + lo parts of that type (two MFMAs per k-step), keeping about 16 (bf16) or 22
+// (fp16) significant bits; for fp16 caches q~ is first multiplied per head by the
+// power of two that brings its largest element to at most 2^14 (exact, scores scaled
+// back), so it cannot overflow.  PV: P (at most 2^8 with the lazy rescale below) also
+// enters as hi + lo parts of the cache type.  Split partials are stored normalised (u_s = acc / l) in
+// fp16 times a per-(head, split) power of two chosen from the largest |u_s| of the
+// head, so they neither overflow nor lose their small values whatever the latent's
+// range (a bf16 latent may hold values far outside fp16's range).
 // LDS tile layout: blocks of 8 logical 16-byte chunks (128 bytes) x 64 rows; inside
 // a block, chunk c of row r sits at slot (c % 8) ^ f(r), where f(r) is the 3-bit
 // reversal of (r >> 1) & 7, so the 16 rows of a QK read and the 8 rows of half a
@@ -188,25 +193,7 @@ __device__ __forceinline__ int row_swizzle(int r) {
     return ((x & 1) << 2) | (x & 2) | (x >> 2);
 }
 
-// Two packed bf16 -> two packed fp16 (v_cvt_pk_f16_f32: exact in the fp16 normal range).
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
-    typedef float f32x2_t __attribute__((ext_vector_type(2)));
-    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    const f32x2_t f = {__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
-}
-
-// QK operand from 16 cache bytes: fp16 as is, bf16 converted to fp16.
-template <bool SRC_BF16>
-__device__ __forceinline__ f16x8_t qk_operand(const U32x4& r) {
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-    const u32x4_t v = SRC_BF16 ? u32x4_t{bf16x2_to_f16x2(r.x), bf16x2_to_f16x2(r.y), bf16x2_to_f16x2(r.z), bf16x2_to_f16x2(r.w)}
-                               : u32x4_t{r.x, r.y, r.z, r.w};
-    return __builtin_bit_cast(f16x8_t, v);
-}
-
-// PV runs in the cache's own 16-bit type: the latent goes to the MFMA unconverted
-// and P is rounded to that type (P is in [0, 1]).
+// MFMA operands in the cache's own 16-bit type.
 template <bool SRC_BF16> struct PvType;
 template <> struct PvType<false> {
     typedef _Float16 elem;
@@ -231,8 +218,8 @@ struct MlaMK {
     const float* q_tilde;
     const float* q_rope;
     float* u;
-    void* part_u;      // [heads][splits][kv_lora] fp16, normalised by l
-    float2* part_ml;   // [heads][splits] (m, l)
+    void* part_u;      // [heads][splits][kv_lora] fp16: u_s / 2^e
+    float4* part_ml;   // [heads][splits] (m, l, e, 0)
     float qscale;      // scale * log2(e)
 };
 
@@ -245,13 +232,12 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     constexpr int NK = W / 32;            // QK k-steps
     constexpr int TB = kMTile * RB;       // tile bytes = CR KiB
     constexpr int DMA_PER_WAVE = CR / 4;  // 1 KiB DMA instructions per wave per tile
-    constexpr int QS = RB + 16;           // row stride of the staged q~ (bytes)
-    static_assert(kMHeads * QS <= TB, "q~ staging must fit in one tile buffer");
+    using MT = PvType<SRC_BF16>;          // MFMA operands in the cache type
 
     __shared__ __attribute__((aligned(1024))) char lds_t0[TB];
     __shared__ __attribute__((aligned(1024))) char lds_t1[TB];
     __shared__ __attribute__((aligned(16))) float lds_s[kMHeads * kScoreStride];
-    __shared__ int lds_qexp[kMHeads];
+    __shared__ float lds_amax[4][kMHeads];
 
     // Launch slot b runs on XCD b % 8; consecutive logical indices (the head groups
     // of one split, then the next split) are kept on one XCD so its L2 serves the
@@ -302,57 +288,52 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     // page of the next tile to copy, loaded one tile ahead
     int phys_next = ntiles > 1 ? p.page_table[(t_begin + kMTile) >> kPageShift] : 0;
 
-    // ---- q~ of the 32 heads: fp32 -> fp16 scaled by 2^-qexp, staged in buffer 1.
-    // Eight consecutive threads share a head; thread `part` takes float4 columns
-    // part, part + 8, ...
+    // ---- B operands of QK, loaded straight into registers: lane (q4, l16) holds dims
+    // 32kk + 8q4 .. +8 of head 16ht + l16 (the wave's head tile ht = w % 2), split into
+    // hi + lo parts of the cache type (fp16: after the per-head power-of-two scaling).
+    const int ht = wave & 1;
+    const int ph = wave >> 1;  // position half of the tile
+    typename MT::vec qhi[NK], qlo[NK];
+    float sscale;
     {
-        const int hl = tid >> 3;
-        const int part = tid & 7;
-        const int head = min(hg * kMHeads + hl, p.heads - 1);
-        float4 v[NK];
+        const int head = min(hg * kMHeads + 16 * ht + l16, p.heads - 1);  // padding heads are never stored
+        float qf[NK][8];
         float amax = 0.f;
 #pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const int d = 4 * (part + 8 * i);
-            v[i] = d < KL ? *reinterpret_cast<const float4*>(p.q_tilde + static_cast<size_t>(head) * KL + d)
-                          : *reinterpret_cast<const float4*>(p.q_rope + static_cast<size_t>(head) * KR + (d - KL));
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        for (int kk = 0; kk < NK; ++kk) {
+            const int d = 32 * kk + 8 * q4;
+            const float* src = d < KL ? p.q_tilde + static_cast<size_t>(head) * KL + d
+                                      : p.q_rope + static_cast<size_t>(head) * KR + (d - KL);
+            const float4 x = *reinterpret_cast<const float4*>(src);
+            const float4 y = *reinterpret_cast<const float4*>(src + 4);
+            qf[kk][0] = x.x; qf[kk][1] = x.y; qf[kk][2] = x.z; qf[kk][3] = x.w;
+            qf[kk][4] = y.x; qf[kk][5] = y.y; qf[kk][6] = y.z; qf[kk][7] = y.w;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qf[kk][i]));
         }
-        amax = fmaxf(amax, dpp_xor1(amax));
-        amax = fmaxf(amax, dpp_xor2(amax));
-        amax = fmaxf(amax, dpp_half_mirror(amax));
         int qexp = 0;
-        if (amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
-        const float down = ldexpf(1.f, -qexp);
-#pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const _Float16 h0 = static_cast<_Float16>(v[i].x * down), h1 = static_cast<_Float16>(v[i].y * down);
-            const _Float16 h2 = static_cast<_Float16>(v[i].z * down), h3 = static_cast<_Float16>(v[i].w * down);
-            const uint2 w2 = make_uint2(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
-                                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16),
-                                        static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h2)) |
-                                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h3)) << 16));
-            *reinterpret_cast<uint2*>(lds_t1 + hl * QS + 8 * (part + 8 * i)) = w2;
+        if (!SRC_BF16) {
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            if (amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
         }
-        if (part == 0) lds_qexp[hl] = qexp;
-    }
-    lds_barrier();
-    // B operands of QK: head 16nt + l16, dims 32kk + 8q4 .. +8
-    f16x8_t qv[2][NK];
-    float sscale[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int hr = 16 * nt + l16;
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk)
-            qv[nt][kk] = *reinterpret_cast<const f16x8_t*>(lds_t1 + hr * QS + 64 * kk + 16 * q4);
-        sscale[nt] = p.qscale * ldexpf(1.f, lds_qexp[hr]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = SRC_BF16 ? qf[kk][i] : ldexpf(qf[kk][i], -qexp);
+                const typename MT::elem hi = static_cast<typename MT::elem>(x);
+                qhi[kk][i] = hi;
+                qlo[kk][i] = static_cast<typename MT::elem>(x - static_cast<float>(hi));
+            }
+        sscale = p.qscale * ldexpf(1.f, qexp);
     }
 
-    // Per-lane LDS offsets (layout of the DMA above).  QK: row 16w + l16, logical
-    // chunk 4kk + q4 = block kk/2, slot 4 (kk & 1) + q4, stored at slot
-    // (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) + (q4 ^ (f & 3)).
-    const int rq = 16 * wave + l16;
+    // Per-lane LDS offsets (layout of the DMA above).  QK: rows 32ph + 16mt + l16,
+    // logical chunk 4kk + q4 = block kk/2, slot 4 (kk & 1) + q4, stored at slot
+    // (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) + (q4 ^ (f & 3)); f depends on
+    // l16 only (32ph + 16mt is a multiple of 16).
+    const int rq = 32 * ph + l16;
     const int fq = row_swizzle(rq);
     const int qk_off = rq * 128 + 16 * (q4 ^ (fq & 3));
     const int qk_flip = fq >> 2;
@@ -386,32 +367,35 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
         if (it + 1 < ntiles) dma(t0 + kMTile, __builtin_amdgcn_readfirstlane(phys_next), next);
         if (it + 2 < ntiles) phys_next = p.page_table[(t0 + 2 * kMTile) >> kPageShift];
 
-        // ---- QK
+        // ---- QK: M tiles mt = positions 32ph + 16mt .. +16, one N tile of 16 heads
         f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-            const U32x4 raw = *reinterpret_cast<const U32x4*>(tile + 8192 * (kk >> 1) + qk_off + 64 * ((kk & 1) ^ qk_flip));
-            const f16x8_t av = qk_operand<SRC_BF16>(raw);
-            sc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qv[0][kk], sc[0], 0, 0, 0);
-            sc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qv[1][kk], sc[1], 0, 0, 0);
-        }
-        // lane holds positions 16w + 4q4 + r of heads 16nt + l16
+        for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+            for (int mt = 0; mt < 2; ++mt) {
+                const U32x4 raw = *reinterpret_cast<const U32x4*>(tile + 8192 * (kk >> 1) + 2048 * mt + qk_off +
+                                                                  64 * ((kk & 1) ^ qk_flip));
+                const auto av = __builtin_bit_cast(typename MT::vec, raw);
+                sc[mt] = MT::mma(av, qhi[kk], sc[mt]);
+                sc[mt] = MT::mma(av, qlo[kk], sc[mt]);
+            }
+        // lane holds positions 32ph + 16mt + 4q4 + r of head 16ht + l16
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
             float4 s4;
-            const int pos = t0 + 16 * wave + 4 * q4;
-            s4.x = pos + 0 < t_end ? sc[nt][0] * sscale[nt] : -INFINITY;
-            s4.y = pos + 1 < t_end ? sc[nt][1] * sscale[nt] : -INFINITY;
-            s4.z = pos + 2 < t_end ? sc[nt][2] * sscale[nt] : -INFINITY;
-            s4.w = pos + 3 < t_end ? sc[nt][3] * sscale[nt] : -INFINITY;
-            *reinterpret_cast<float4*>(lds_s + (16 * nt + l16) * kScoreStride + 16 * wave + 4 * q4) = s4;
+            const int pos = t0 + 32 * ph + 16 * mt + 4 * q4;
+            s4.x = pos + 0 < t_end ? sc[mt][0] * sscale : -INFINITY;
+            s4.y = pos + 1 < t_end ? sc[mt][1] * sscale : -INFINITY;
+            s4.z = pos + 2 < t_end ? sc[mt][2] * sscale : -INFINITY;
+            s4.w = pos + 3 < t_end ? sc[mt][3] * sscale : -INFINITY;
+            *reinterpret_cast<float4*>(lds_s + (16 * ht + l16) * kScoreStride + 32 * ph + 16 * mt + 4 * q4) = s4;
         }
         lds_barrier_dma_in_flight();
 
         // ---- softmax over the 64 positions; P^T operands: k-slot 8q4 + i of step ks
         // is position 32ks + 4q4 + i (i < 4) or 32ks + 16 + 4q4 + i - 4
-        using PV = PvType<SRC_BF16>;
-        typename PV::vec pb[2][2];
+        using PV = MT;
+        typename PV::vec pb[2][2], pl[2][2];  // P as hi + lo parts of the cache type
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             float s[2][8];
@@ -447,7 +431,9 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
                 for (int i = 0; i < 8; ++i) {
                     const float e = fast_exp2(s[ks][i] - mref);
                     l[nt] += e;
-                    pb[nt][ks][i] = static_cast<typename PV::elem>(e);
+                    const typename PV::elem hi = static_cast<typename PV::elem>(e);
+                    pb[nt][ks][i] = hi;
+                    pl[nt][ks][i] = static_cast<typename PV::elem>(e - static_cast<float>(hi));
                 }
         }
 
@@ -467,7 +453,9 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
                 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
                 const auto av = __builtin_bit_cast(typename PV::vec, u32x4_t{lw.x, lw.y, hw.x, hw.y});
                 acc[0][dt] = PV::mma(av, pb[0][ks], acc[0][dt]);
+                acc[0][dt] = PV::mma(av, pl[0][ks], acc[0][dt]);
                 acc[1][dt] = PV::mma(av, pb[1][ks], acc[1][dt]);
+                acc[1][dt] = PV::mma(av, pl[1][ks], acc[1][dt]);
             }
     };
     for (int it = 0; it < ntiles; it += 2) {
@@ -496,30 +484,49 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
         }
         return;
     }
-    // Normalised split result u_s = acc / l in fp16 (a convex combination of latent rows,
-    // so inside the fp16 range the QK operands already need).  A lane holds 4 dims of each
-    // of 8 dim tiles of its head, so it would store 8 bytes into each of 16 head rows per
+    // Normalised split result u_s = acc / l, stored as fp16 u_s / 2^e with e per (head,
+    // split) such that the head's largest |u_s| lands in [2^14, 2^15): no overflow and
+    // full fp16 precision whatever the latent's range.  A lane holds 4 dims of each of 8
+    // dim tiles of its head, so it would store 8 bytes into each of 16 head rows per
     // instruction; the rows are assembled in LDS first (tile buffer 0, free after the
     // barrier) and every wave store then writes one whole 1 KiB head row.
     constexpr int SR = KL * 2 + 16;  // staged row pitch (bytes)
     static_assert(kMHeads * SR <= TB, "staged partials must fit in one tile buffer");
-    lds_barrier();  // every wave is done with the last tile
+    float inv[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        inv[nt] = 1.f / l[nt];
+        float amax = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(acc[nt][dt][r] * inv[nt]));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (q4 == 0) lds_amax[wave][16 * nt + l16] = amax;
+    }
+    lds_barrier();  // every wave is done with the last tile; lds_amax is complete
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int hl = 16 * nt + l16;
-        const float inv = 1.f / l[nt];
+        const float amax = fmaxf(fmaxf(lds_amax[0][hl], lds_amax[1][hl]), fmaxf(lds_amax[2][hl], lds_amax[3][hl]));
+        // e = floor(log2(amax)) - 14 for finite non-zero amax (subnormals included)
+        const int e = amax > 0.f && amax <= 3.4e38f ? ilogbf(amax) - 14 : 0;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             typedef float f32x2_t __attribute__((ext_vector_type(2)));
             typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-            const f16x2_t lo = __builtin_convertvector(f32x2_t{acc[nt][dt][0] * inv, acc[nt][dt][1] * inv}, f16x2_t);
-            const f16x2_t hi = __builtin_convertvector(f32x2_t{acc[nt][dt][2] * inv, acc[nt][dt][3] * inv}, f16x2_t);
+            const f16x2_t lo = __builtin_convertvector(
+                f32x2_t{ldexpf(acc[nt][dt][0] * inv[nt], -e), ldexpf(acc[nt][dt][1] * inv[nt], -e)}, f16x2_t);
+            const f16x2_t hi = __builtin_convertvector(
+                f32x2_t{ldexpf(acc[nt][dt][2] * inv[nt], -e), ldexpf(acc[nt][dt][3] * inv[nt], -e)}, f16x2_t);
             *reinterpret_cast<uint2*>(lds_t0 + hl * SR + 2 * (128 * wave + 16 * dt + 4 * q4)) =
                 make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
         }
         const int head = hg * kMHeads + hl;
         if (wave == 0 && q4 == 0 && head < p.heads)
-            p.part_ml[static_cast<size_t>(head) * p.splits + split] = make_float2(m[nt], l[nt]);
+            p.part_ml[static_cast<size_t>(head) * p.splits + split] =
+                make_float4(m[nt], l[nt], static_cast<float>(e), 0.f);
     }
     lds_barrier();
     // wave w writes head rows w, w + 4, ...: lane j the 16 bytes at 16 j
@@ -536,7 +543,7 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
 
 // Split merge for the MFMA path: one workgroup per (head, 128-dim block); a thread
 // owns 4 dims of the block and every 8th split, loading 8 normalised fp16 partials
-// at a time; split s weighs l_s 2^(m_s - M).
+// at a time; split s weighs l_s 2^(m_s - M) and its stored values 2^e_s.
 __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
     constexpr int KL = kMfmaLora;
     const int h = blockIdx.x;
@@ -550,13 +557,13 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = grp; s0 < p.splits; s0 += 64) {
         uint2 a[8];
-        float2 ml[8];
+        float4 ml[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int s = s0 + 8 * i;
             const bool in = s < p.splits;
             a[i] = in ? *reinterpret_cast<const uint2*>(part + (base + s) * KL + d) : make_uint2(0u, 0u);
-            ml[i] = in ? p.part_ml[base + s] : make_float2(-INFINITY, 0.f);
+            ml[i] = in ? p.part_ml[base + s] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
         }
         float mb = m;
 #pragma unroll
@@ -567,14 +574,15 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float w = ml[i].x == -INFINITY ? 0.f : ml[i].y * fast_exp2(ml[i].x - mb);
+            const float wv = ldexpf(w, static_cast<int>(ml[i].z));  // weight of the stored values
             typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
             const f16x2_t lo = __builtin_bit_cast(f16x2_t, a[i].x);
             const f16x2_t hi = __builtin_bit_cast(f16x2_t, a[i].y);
             l += w;
-            o.x = fmaf(static_cast<float>(lo[0]), w, o.x);
-            o.y = fmaf(static_cast<float>(lo[1]), w, o.y);
-            o.z = fmaf(static_cast<float>(hi[0]), w, o.z);
-            o.w = fmaf(static_cast<float>(hi[1]), w, o.w);
+            o.x = fmaf(static_cast<float>(lo[0]), wv, o.x);
+            o.y = fmaf(static_cast<float>(lo[1]), wv, o.y);
+            o.z = fmaf(static_cast<float>(hi[0]), wv, o.z);
+            o.w = fmaf(static_cast<float>(hi[1]), wv, o.w);
         }
         m = mb;
     }
@@ -641,8 +649,9 @@ MlaPlan plan_mla(const MlaArgs& a) {
     }
     pl.splits = (a.seq_len + pl.split_tokens - 1) / pl.split_tokens;
     const size_t slots = static_cast<size_t>(a.heads) * pl.splits;
-    const size_t part_elem = mfma_eligible(a) ? 2 : 4;  // fp16 partials on the MFMA path
-    pl.workspace_bytes = (pl.splits > 1 ? align256(slots * a.kv_lora * part_elem) + align256(slots * 8) : 0) + q_copy;
+    const size_t part_elem = mfma_eligible(a) ? 2 : 4;   // fp16 partials on the MFMA path
+    const size_t ml_bytes = mfma_eligible(a) ? 16 : 8;  // (m, l, e, 0) / (m, l)
+    pl.workspace_bytes = (pl.splits > 1 ? align256(slots * a.kv_lora * part_elem) + align256(slots * ml_bytes) : 0) + q_copy;
     return pl;
 }
 
@@ -669,9 +678,9 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
         k.groups = (a.heads + kMHeads - 1) / kMHeads;
         k.per_xcd = (k.groups * pl.splits + 7) / 8;
         k.u = a.u;
-        const size_t part_bytes = pl.splits > 1 ? align256(slots * a.kv_lora * 2) + align256(slots * 8) : 0;
+        const size_t part_bytes = pl.splits > 1 ? align256(slots * a.kv_lora * 2) + align256(slots * 16) : 0;
         k.part_u = ws;
-        k.part_ml = reinterpret_cast<float2*>(ws + align256(slots * a.kv_lora * 2));
+        k.part_ml = reinterpret_cast<float4*>(ws + align256(slots * a.kv_lora * 2));
         // the kernel reads q~ / q_rope as float4
         k.q_tilde = a.q_tilde;
         k.q_rope = a.q_rope;

@@ -1,9 +1,11 @@
 """GPU parity of the MLA absorbed path (MlaLatentCache.cs:29-65, StreamingEngine.cs:508-577).
 
 Tolerances: fp32 latents (generic kernel, fp32 accumulation): max-abs <= 1e-3,
-rel-L2 <= 1e-4.  16-bit latents on MFMA tiles (fp16 operands for q~ and P, fp32
-accumulation): max-abs <= 1e-3, rel-L2 <= 5e-3 against the oracle fed the same
-16-bit latent values.  Both sides' errors against fp64 are printed.
+rel-L2 <= 1e-4.  16-bit latents on MFMA tiles (operands in the cache's 16-bit type,
+q~ as hi + lo parts, P rounded to the cache type, fp32 accumulation): max-abs <= 1e-3,
+rel-L2 <= 5e-3 against the oracle fed the same 16-bit latent values; for latents far
+from unit scale the max-abs bound is 1e-3 times the largest output magnitude.  Both
+sides' errors against fp64 are printed.
 """
 import math
 
@@ -152,3 +154,45 @@ def test_mla_dev_entry_with_unaligned_queries(gpu):
     got = u.cpu().numpy().reshape(heads, 512)
     assert np.array_equal(got, aligned)
     check_mla(got, latd, qt, qrp, 512, 64, scale, 5e-3, "unaligned q")
+
+
+@pytest.mark.parametrize("case", ["spikes", "all_large", "all_tiny"])
+def test_mla_bf16_latents_outside_the_fp16_range(gpu, case):
+    """bf16 latents hold any finite fp32 exponent (the reference keeps fp32 latents,
+    MlaLatentCache.cs:45-51, StreamingEngine.cs:531-568): elements at +-1e5 and +-1e-6
+    among N(0,1) ones, a whole cache scaled by 1e6 (outputs far past fp16's 65504, with
+    several splits), and one scaled by 1e-6 (fp16 subnormals).  The spiked columns get a
+    zero query weight, so the 1e5 values pass through every QK product (an fp16 operand
+    would turn them into inf, and inf * 0 into NaN) and through the latent sum, while the
+    scores stay well conditioned (a score of 1e4 would make the softmax depend on its
+    last bits, beyond what either fp32 side resolves)."""
+    heads, kv_lora, rope, n = 128, 512, 64, 4096
+    rng = np.random.default_rng(1234)
+    lat = rng.standard_normal((n, kv_lora + rope), dtype=np.float32)
+    qt = rng.standard_normal((heads, kv_lora), dtype=np.float32)
+    qrp = rng.standard_normal((heads, rope), dtype=np.float32)
+    if case == "spikes":
+        cols = rng.choice(kv_lora + rope, 24, replace=False)
+        for k, val in enumerate((1e5, -1e5, 1e-6, -1e-6)):
+            lat[rng.integers(0, n, 40), np.repeat(cols[6 * k:6 * k + 6], 40 // 6 + 1)[:40]] = val
+        qt[:, cols[cols < kv_lora]] = 0.0
+        qrp[:, cols[cols >= kv_lora] - kv_lora] = 0.0
+    elif case == "all_large":
+        lat *= 1e6
+        qt *= 1e-6
+        qrp *= 1e-6
+    else:
+        lat *= 1e-6
+        qt *= 1e6
+        qrp *= 1e6
+    bits, latd = to_dtype_bits(lat, "bf16")
+    scale = 1 / math.sqrt(192)
+    with qr.MlaLatentCache(1, kv_lora, rope, n, dtype="bf16") as m:
+        m.AppendRange(0, 0, bits, src_dtype="bf16")
+        got = m.AbsorbedAttention(0, n - 1, qt, qrp, scale)
+    want = oracle.mla_attention(latd, qt, qrp, kv_lora, rope, scale)
+    assert np.isfinite(got).all(), f"{case}: non-finite output"
+    a, r = assert_close(got, want, 1e-3 * max(1.0, float(np.max(np.abs(want)))), 5e-3, f"bf16 range {case}")
+    f64 = oracle.mla_attention_f64(latd, qt, qrp, kv_lora, rope, scale)
+    print(f"bf16 range {case}: max |u| {np.max(np.abs(want)):.3e}, vs oracle max-abs {a:.2e} rel {r:.2e} | "
+          f"vs fp64: gpu {errors(got, f64)[1]:.2e} oracle {errors(want, f64)[1]:.2e}")
