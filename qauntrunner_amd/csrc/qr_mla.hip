@@ -238,6 +238,7 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     __shared__ __attribute__((aligned(1024))) char lds_t1[TB];
     __shared__ __attribute__((aligned(16))) float lds_s[kMHeads * kScoreStride];
     __shared__ float lds_amax[4][kMHeads];
+    __shared__ int lds_qexp[kMHeads];
 
     // Launch slot b runs on XCD b % 8; consecutive logical indices (the head groups
     // of one split, then the next split) are kept on one XCD so its L2 serves the
@@ -288,45 +289,68 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     // page of the next tile to copy, loaded one tile ahead
     int phys_next = ntiles > 1 ? p.page_table[(t_begin + kMTile) >> kPageShift] : 0;
 
-    // ---- B operands of QK, loaded straight into registers: lane (q4, l16) holds dims
-    // 32kk + 8q4 .. +8 of head 16ht + l16 (the wave's head tile ht = w % 2), split into
-    // hi + lo parts of the cache type (fp16: after the per-head power-of-two scaling).
+    // ---- B operands of QK: lane (q4, l16) holds dims 32kk + 8q4 .. +8 of head 16ht + l16
+    // (the wave's head tile ht = w % 2), split into hi + lo parts of the cache type (fp16:
+    // after the per-head power-of-two scaling).  q~ of the workgroup's 32 heads is read
+    // once, coalesced, converted to hi + lo and staged in tile buffer 1 (free until the
+    // second tile's copy), then every wave reads its 16 heads' operands from there.
     const int ht = wave & 1;
     const int ph = wave >> 1;  // position half of the tile
-    typename MT::vec qhi[NK], qlo[NK];
-    float sscale;
+    // staged rows of one part: W * 2 bytes, 16-byte chunk c of row r at chunk c ^ (r & 7)
+    // (W / 8 is a multiple of 8), so the 16 rows of one operand read use distinct banks
+    constexpr int QS = W * 2;
+    static_assert(2 * kMHeads * QS <= TB, "q~ hi + lo staging must fit in one tile buffer");
     {
-        const int head = min(hg * kMHeads + 16 * ht + l16, p.heads - 1);  // padding heads are never stored
-        float qf[NK][8];
+        // eight threads per head, thread `part` takes float4 columns part, part + 8, ...
+        const int hl = tid >> 3;
+        const int part = tid & 7;
+        const int head = min(hg * kMHeads + hl, p.heads - 1);  // padding heads are never stored
+        float4 v[NK];
         float amax = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-            const int d = 32 * kk + 8 * q4;
-            const float* src = d < KL ? p.q_tilde + static_cast<size_t>(head) * KL + d
-                                      : p.q_rope + static_cast<size_t>(head) * KR + (d - KL);
-            const float4 x = *reinterpret_cast<const float4*>(src);
-            const float4 y = *reinterpret_cast<const float4*>(src + 4);
-            qf[kk][0] = x.x; qf[kk][1] = x.y; qf[kk][2] = x.z; qf[kk][3] = x.w;
-            qf[kk][4] = y.x; qf[kk][5] = y.y; qf[kk][6] = y.z; qf[kk][7] = y.w;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qf[kk][i]));
+        for (int i = 0; i < NK; ++i) {
+            const int d = 4 * (part + 8 * i);
+            v[i] = d < KL ? *reinterpret_cast<const float4*>(p.q_tilde + static_cast<size_t>(head) * KL + d)
+                          : *reinterpret_cast<const float4*>(p.q_rope + static_cast<size_t>(head) * KR + (d - KL));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
         }
         int qexp = 0;
         if (!SRC_BF16) {
-            amax = fmaxf(amax, __shfl_xor(amax, 16));
-            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            amax = fmaxf(amax, dpp_xor1(amax));
+            amax = fmaxf(amax, dpp_xor2(amax));
+            amax = fmaxf(amax, dpp_half_mirror(amax));
             if (amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
         }
+        typedef typename MT::elem E;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk)
+        for (int i = 0; i < NK; ++i) {
+            const float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            E hi[4], lo[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = SRC_BF16 ? qf[kk][i] : ldexpf(qf[kk][i], -qexp);
-                const typename MT::elem hi = static_cast<typename MT::elem>(x);
-                qhi[kk][i] = hi;
-                qlo[kk][i] = static_cast<typename MT::elem>(x - static_cast<float>(hi));
+            for (int c = 0; c < 4; ++c) {
+                const float y = SRC_BF16 ? x[c] : ldexpf(x[c], -qexp);
+                hi[c] = static_cast<E>(y);
+                lo[c] = static_cast<E>(y - static_cast<float>(hi[c]));
             }
-        sscale = p.qscale * ldexpf(1.f, qexp);
+            const int col = part + 8 * i;  // 8-byte column: chunk col / 2, half col % 2
+            char* row = lds_t1 + hl * QS + 16 * ((col >> 1) ^ (hl & 7)) + 8 * (col & 1);
+            *reinterpret_cast<uint2*>(row) = __builtin_bit_cast(uint2, hi);
+            *reinterpret_cast<uint2*>(row + kMHeads * QS) = __builtin_bit_cast(uint2, lo);
+        }
+        if (part == 0) lds_qexp[hl] = qexp;
+    }
+    lds_barrier();
+    typename MT::vec qhi[NK], qlo[NK];
+    float sscale;
+    {
+        const int hr = 16 * ht + l16;
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+            const int c = (4 * kk + q4) ^ (hr & 7);
+            qhi[kk] = *reinterpret_cast<const typename MT::vec*>(lds_t1 + hr * QS + 16 * c);
+            qlo[kk] = *reinterpret_cast<const typename MT::vec*>(lds_t1 + (kMHeads + hr) * QS + 16 * c);
+        }
+        sscale = p.qscale * ldexpf(1.f, lds_qexp[hr]);
     }
 
     // Per-lane LDS offsets (layout of the DMA above).  QK: rows 32ph + 16mt + l16,
@@ -363,12 +387,15 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     auto step = [&](int it, const char* tile, char* next) __attribute__((always_inline)) {
         const int t0 = t_begin + it * kMTile;
         wait_dma();
-        lds_barrier();  // tile `it` is in LDS; tile it-1 and its scores are consumed
+        lds_barrier();  // tile `it` is in LDS; tile it-1 (or the staged q~), its scores are consumed
         if (it + 1 < ntiles) dma(t0 + kMTile, __builtin_amdgcn_readfirstlane(phys_next), next);
         if (it + 2 < ntiles) phys_next = p.page_table[(t0 + 2 * kMTile) >> kPageShift];
 
         // ---- QK: M tiles mt = positions 32ph + 16mt .. +16, one N tile of 16 heads
-        f32x4_t sc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+        // hi and lo products go to separate accumulators: four independent MFMA chains
+        f32x4_t sc[2], sl[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) sc[mt] = sl[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
@@ -377,8 +404,10 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
                                                                   64 * ((kk & 1) ^ qk_flip));
                 const auto av = __builtin_bit_cast(typename MT::vec, raw);
                 sc[mt] = MT::mma(av, qhi[kk], sc[mt]);
-                sc[mt] = MT::mma(av, qlo[kk], sc[mt]);
+                sl[mt] = MT::mma(av, qlo[kk], sl[mt]);
             }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) sc[mt] += sl[mt];
         // lane holds positions 32ph + 16mt + 4q4 + r of head 16ht + l16
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
