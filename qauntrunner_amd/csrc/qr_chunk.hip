@@ -62,6 +62,9 @@ struct ChunkK {
     int queries_per_block;
     int split_tokens;        // multiple of kTile
     int splits;
+    int qblocks;
+    int units;               // splits x qblocks x kv_heads
+    int per_xcd;             // launch slots per XCD: ceil(units / 8)
 };
 
 // BF16: cache element type; NT: 16-row N tiles per wave; NSTAGE: LDS tile buffers;
@@ -82,9 +85,18 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
 
     __shared__ __attribute__((aligned(1024))) char lds[NSTAGE][KB + VB];
 
-    const int split = blockIdx.x;
-    const int qblk = blockIdx.y;
-    const int kvh = blockIdx.z;
+    // Launch slot b runs on XCD b % 8 (round-robin dispatch); XCD x takes the contiguous
+    // logical units [x per_xcd, (x + 1) per_xcd), ordered split fastest, then query
+    // block, then kv head, so the query blocks of one kv head share one XCD and its L2
+    // keeps that kv head's K/V (4 MB at 8192 positions, head_dim 128) instead of every
+    // L2 cycling through all kv heads.  Query blocks run from the last (most keys under
+    // the causal mask) to the first, so the longest units start first.
+    const int bslot = blockIdx.x;
+    const int unit = (bslot & 7) * p.per_xcd + (bslot >> 3);
+    if (unit >= p.units) return;
+    const int split = unit % p.splits;
+    const int qblk = p.qblocks - 1 - (unit / p.splits) % p.qblocks;
+    const int kvh = unit / (p.splits * p.qblocks);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
     const int q4 = lane >> 4;
@@ -457,7 +469,10 @@ hipError_t launch_chunk(const ChunkArgs& a, const ChunkPlan& pl, void* workspace
     k.queries_per_block = pl.queries_per_block;
     k.split_tokens = pl.split_tokens;
     k.splits = pl.splits;
-    const dim3 grid(pl.splits, pl.qblocks, a.geom.kv_heads);
+    k.qblocks = pl.qblocks;
+    k.units = pl.splits * pl.qblocks * a.geom.kv_heads;
+    k.per_xcd = (k.units + 7) / 8;
+    const dim3 grid(8 * k.per_xcd);
     const bool bf = a.kv_dtype == QR_DTYPE_BF16;
     const bool qsplit = a.q_dtype != a.kv_dtype;  // q not exact in the cache's 16-bit type
     hipError_t e;
