@@ -295,7 +295,7 @@ def run_gpu(w, steps, warmup):
         width = w["kv_lora"] + w["rope_dim"]
         set_bytes = w["n"] * width * esize(w["dtype"])
         R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
-        cache = qr.MlaLatentCache(R, w["kv_lora"], w["rope_dim"], w["n"], dtype=w["dtype"])
+        cache = qr.MlaLatentCache(R, w["kv_lora"] + w["rope_dim"], w["n"], dtype=w["dtype"], rope=w["rope_dim"])
         cache.Reserve(R * math.ceil(w["n"] / 256))
         for layer in range(R):
             rows = torch.randn(w["n"], width, device=dev, generator=gen)
@@ -320,7 +320,7 @@ def run_gpu(w, steps, warmup):
         code = KVB_FORMATS[w["kvb_fmt"]][0]
         set_bytes = w["n"] * width * esize(w["dtype"]) + kvb_bytes(w)
         R = max(1, math.ceil(ROTATE_BYTES / set_bytes))
-        cache = qr.MlaLatentCache(R, L, w["rope_dim"], w["n"], dtype=w["dtype"])
+        cache = qr.MlaLatentCache(R, L + w["rope_dim"], w["n"], dtype=w["dtype"], rope=w["rope_dim"])
         cache.Reserve(R * math.ceil(w["n"] / 256))
         kvbs = []
         for layer in range(R):

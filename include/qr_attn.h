@@ -82,8 +82,10 @@ const char* qr_status_name(int status);
 /* ctor PagedKvCache(layers, heads, kvHeads, headDim, maxSeq), PagedKvCache.cs:29-37.
  * kv_dtype: QR_DTYPE_F32 (the reference's page type, PagedKvCache.cs:17-18),
  * F16 or BF16.  max_batch: number of independent sequences (seq_id 0..max_batch-1),
- * each with its own page table; 1 reproduces the reference.  head_dim must be
- * one of 16, 32, 64, 128, 256. */
+ * each with its own page table; 1 reproduces the reference.  head_dim: a multiple
+ * of 8 from 16 to 256 (the reference takes any; model head sizes are multiples of 8).
+ * 16-bit caches with head_dim 64 or 128 decode on MFMA tiles; every other shape on the
+ * fp32 streaming kernel. */
 int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim, int max_seq,
                  int kv_dtype, int max_batch);
 int qr_kv_destroy(qr_kv* kv);
@@ -195,12 +197,24 @@ int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, v
 
 /* ---- MlaLatentCache ---------------------------------------------------- */
 
-/* ctor MlaLatentCache(layers, latentDim, maxSeq), MlaLatentCache.cs:22-27, with
- * latentDim = kv_lora + rope (StreamingEngine.cs:96).  dtype: F32, F16 or BF16.
- * 1 <= kv_lora <= 1024, 0 <= rope <= 256.  16-bit caches with kv_lora 512 and rope
- * 0 or 64 run on MFMA tiles with fp16 operands (bf16 latents must lie in the fp16
- * range, |x| < 65504); every other shape runs a generic fp32 kernel. */
+/* ctor MlaLatentCache(layers, latentDim, maxSeq), MlaLatentCache.cs:22-27, with the
+ * latent split given up front: latentDim = kv_lora + rope (StreamingEngine.cs:96).
+ * dtype: F32, F16 or BF16.  1 <= kv_lora <= 1024, 0 <= rope <= 256.  16-bit caches
+ * with kv_lora 512 and rope 0 or 64 run on MFMA tiles whose operands stay in the
+ * cache's 16-bit type (any finite latent value); every other shape runs a generic
+ * fp32 kernel. */
 int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, int dtype);
+/* ctor MlaLatentCache(layers, latentDim, maxSeq) exactly as the reference takes it
+ * (MlaLatentCache.cs:22; StreamingEngine.cs:96-97 passes kv_lora + rope): storage
+ * needs the row width only.  The cache knows no kv_lora / rope split (the reference's
+ * split lives in MlaLayer, StreamingEngine.cs:531-568), so attention calls return
+ * QR_ERR_INVALID_ARGUMENT until qr_mla_set_rope fixes it.  latentDim <= 1280. */
+int qr_mla_create_latent(qr_mla** out, int layers, int latent_dim, int max_seq, int dtype);
+/* No reference counterpart: the rope width of the latent rows (kv_lora = latentDim -
+ * rope), as MlaLayer knows it (Config.QkRopeHeadDim); may be set again at any time. */
+int qr_mla_set_rope(qr_mla* m, int rope);
+/* MaxSeq, MlaLatentCache.cs:65. */
+int qr_mla_max_seq(const qr_mla* m, int* out);
 int qr_mla_destroy(qr_mla* mla);
 int qr_mla_reserve(qr_mla* mla, int pages);
 /* Append(layer, pos, latent), MlaLatentCache.cs:45-51 (row of `len` floats <= latentDim). */

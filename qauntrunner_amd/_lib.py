@@ -92,6 +92,9 @@ SIGNATURES = {
     "qr_kv_bytes_per_token": [_p, _llp],
     "qr_kv_read": [_p, _i, _i, _i, _i, _p, _p],
     "qr_mla_create": [_pp, _i, _i, _i, _i, _i],
+    "qr_mla_create_latent": [_pp, _i, _i, _i, _i],
+    "qr_mla_set_rope": [_p, _i],
+    "qr_mla_max_seq": [_p, _ip],
     "qr_mla_destroy": [_p],
     "qr_mla_reserve": [_p, _i],
     "qr_mla_append": [_p, _i, _i, _p, _i],

@@ -288,18 +288,37 @@ class PagedKvCache:
 
 class MlaLatentCache:
     """Paged MLA latent store with absorbed attention (MlaLatentCache.cs:10-65,
-    StreamingEngine.cs:531-568)."""
+    StreamingEngine.cs:531-568).
+
+    MlaLatentCache(layers, latentDim, maxSeq) as the reference's constructor takes it;
+    `rope` (the k_pe width at the end of each latent row) splits the row for attention
+    and may instead be set later with SetRope, as MlaLayer knows it."""
 
     PageTokens = PAGE_TOKENS
 
-    def __init__(self, layers, kv_lora, rope, max_seq, dtype="f32"):
+    def __init__(self, layers, latent_dim, max_seq, dtype="f32", rope=None):
         self._lib = _lib.load()
         h = ctypes.c_void_p()
-        check(self._lib.qr_mla_create(ctypes.byref(h), layers, kv_lora, rope, max_seq, dtype_code(dtype)))
+        if rope is None:
+            check(self._lib.qr_mla_create_latent(ctypes.byref(h), layers, latent_dim, max_seq, dtype_code(dtype)))
+        else:
+            check(self._lib.qr_mla_create(ctypes.byref(h), layers, latent_dim - rope, rope, max_seq,
+                                          dtype_code(dtype)))
         self._h = h
-        self.Layers, self.KvLora, self.Rope, self.MaxSeq = layers, kv_lora, rope, max_seq
-        self.LatentDim = kv_lora + rope
+        self.Layers, self.MaxSeq = layers, max_seq
+        self.LatentDim = latent_dim
+        self.Rope = rope
+        self.KvLora = latent_dim - rope if rope is not None else None
         self.Dtype = dtype_code(dtype)
+
+    def SetRope(self, rope) -> None:
+        check(self._lib.qr_mla_set_rope(self._h, rope))
+        self.Rope, self.KvLora = rope, self.LatentDim - rope
+
+    def max_seq(self) -> int:
+        out = ctypes.c_int()
+        check(self._lib.qr_mla_max_seq(self._h, ctypes.byref(out)))
+        return out.value
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:
@@ -367,14 +386,20 @@ class MlaLatentCache:
     def Truncate(self, length) -> None:
         check(self._lib.qr_mla_truncate(self._h, length))
 
+    def _split(self):
+        """(kv_lora, rope); before SetRope on a cache made from its latent width alone, the
+        whole row -- the library then rejects attention calls until the split is set."""
+        return (self.KvLora, self.Rope) if self.Rope is not None else (self.LatentDim, 0)
+
     def AbsorbedAttention(self, layer, pos, q_tilde, q_rope, scale) -> np.ndarray:
         """u [heads, kv_lora] = softmax(q~.c + q_rope.k_pe) . c over positions 0..pos."""
+        kv_lora, rope = self._split()
         qt = np.ascontiguousarray(q_tilde, dtype=np.float32)
-        heads = qt.size // self.KvLora
-        qr = np.ascontiguousarray(q_rope if self.Rope else np.zeros(1), dtype=np.float32)
-        if self.Rope and qr.size != heads * self.Rope:
+        heads = qt.size // kv_lora
+        qr = np.ascontiguousarray(q_rope if rope else np.zeros(1), dtype=np.float32)
+        if rope and qr.size != heads * rope:
             raise ValueError("q_rope must be [heads, rope]")
-        u = np.empty((heads, self.KvLora), np.float32)
+        u = np.empty((heads, kv_lora), np.float32)
         check(self._lib.qr_mla_attention(self._h, layer, pos, heads, _ptr(qt), _ptr(qr), scale, _ptr(u)))
         return u
 
@@ -383,7 +408,7 @@ class MlaLatentCache:
         nope+rope] (rope part rotated), kvb a Weight of [heads*(nope+vdim), kv_lora].
         Returns the attention output [heads, vdim]."""
         q = np.ascontiguousarray(q, dtype=np.float32)
-        heads = q.size // (nope + self.Rope)
+        heads = q.size // (nope + self._split()[1])
         out = np.empty((heads, vdim), np.float32)
         check(self._lib.qr_mla_attend_absorbed(self._h, layer, pos, heads, nope, vdim, _ptr(q), kvb.handle,
                                                _ptr(out)))
@@ -393,17 +418,19 @@ class MlaLatentCache:
         """Device form: q, out torch tensors on the GPU; kvb a Weight or a uint8 device tensor
         of rows in format `fmt`."""
         f32 = _lib.DTYPE_F32
-        heads = _rows_of(q, nope + self.Rope, "q")
-        qp = _dev_tensor(q, heads * (nope + self.Rope), f32, "q")
+        rope = self._split()[1]
+        heads = _rows_of(q, nope + rope, "q")
+        qp = _dev_tensor(q, heads * (nope + rope), f32, "q")
         op = _dev_tensor(out, heads * vdim, f32, "out")
         check(self._lib.qr_mla_attend_absorbed_dev(self._h, layer, pos, heads, nope, vdim, qp, _dev_ptr(kvb), fmt,
                                                    op, _stream_ptr(stream)))
 
     def AbsorbedAttentionDev(self, layer, pos, q_tilde, q_rope, u, scale, stream=None) -> None:
         f32 = _lib.DTYPE_F32
-        heads = _rows_of(q_tilde, self.KvLora, "q_tilde")
-        qt = _dev_tensor(q_tilde, heads * self.KvLora, f32, "q_tilde")
-        qr_ptr = _dev_tensor(q_rope, heads * self.Rope, f32, "q_rope", allow_none=self.Rope == 0)
-        up = _dev_tensor(u, heads * self.KvLora, f32, "u")
+        kv_lora, rope = self._split()
+        heads = _rows_of(q_tilde, kv_lora, "q_tilde")
+        qt = _dev_tensor(q_tilde, heads * kv_lora, f32, "q_tilde")
+        qr_ptr = _dev_tensor(q_rope, heads * rope, f32, "q_rope", allow_none=rope == 0)
+        up = _dev_tensor(u, heads * kv_lora, f32, "u")
         check(self._lib.qr_mla_attention_dev(self._h, layer, pos, heads, qt, qr_ptr, scale, up,
                                              _stream_ptr(stream)))

@@ -133,6 +133,13 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     // the previous step's loads were still writing, and waited for every load in
     // flight -- the whole prefetch -- once per loop iteration.)
     const uint32_t lane_off = static_cast<uint32_t>((row_in_step * D + sub * EPC) * ESZ);
+    // Head sizes that are a multiple of 8 but not a power of two (80, 96, ...) round the
+    // lanes per row up to a power of two: a chunk past the row end gets an offset beyond
+    // the buffer range, which loads zeros without touching memory, and a zero q slice.
+    constexpr uint32_t kOutOfRange = 0xF0000000u;
+    bool chunk_on[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) chunk_on[j] = DT != 0 || (sub + LPT * j) * EPC < D;
 
     U32x4 kbuf[kPrefetch + 1][UMAX][NC];
     U32x4 vbuf[kPrefetch + 1][UMAX][NC];
@@ -156,11 +163,15 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
         for (int u = 0; u < UMAX; ++u) {
             const uint32_t off = lane_off + static_cast<uint32_t>(u * ntg * D * ESZ);
 #pragma unroll
-            for (int j = 0; j < NC; ++j)
-                kb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + LPT * j * 16, 0, 0));
+            for (int j = 0; j < NC; ++j) {
+                const uint32_t o = chunk_on[j] ? off + LPT * j * 16 : kOutOfRange;
+                kb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
+            }
 #pragma unroll
-            for (int j = 0; j < NC; ++j)
-                vb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + LPT * j * 16, vplane, 0));
+            for (int j = 0; j < NC; ++j) {
+                const uint32_t o = chunk_on[j] ? off + LPT * j * 16 : kOutOfRange;
+                vb[u][j] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, vplane, 0));
+            }
         }
     };
 
@@ -245,7 +256,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
             for (int e = 0; e < EPC; ++e) {
                 const int dim = (sub + LPT * j) * EPC + e;
                 const int h = min(h0 + g, p.heads - 1);  // rows past the unit's heads are read, then zeroed
-                q[g][j * EPC + e] = qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f);
+                q[g][j * EPC + e] = chunk_on[j] ? qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f) : 0.f;
             }
 
 #pragma unroll

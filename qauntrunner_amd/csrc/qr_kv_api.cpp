@@ -183,8 +183,8 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
     QR_CHECK_ARG(layers >= 1, "layers must be >= 1 (got %d)", layers);
     QR_CHECK_ARG(heads >= 1 && kv_heads >= 1 && kv_heads <= heads,
                  "need 1 <= kv_heads <= heads (got heads=%d kv_heads=%d)", heads, kv_heads);
-    QR_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256,
-                 "head_dim %d unsupported (16, 32, 64, 128 or 256)", head_dim);
+    QR_CHECK_ARG(head_dim >= 16 && head_dim <= 256 && head_dim % 8 == 0,
+                 "head_dim %d unsupported (a multiple of 8 from 16 to 256)", head_dim);
     QR_CHECK_ARG(max_seq >= 1, "max_seq must be >= 1 (got %d)", max_seq);
     QR_CHECK_ARG(dtype_valid(kv_dtype), "unknown kv dtype %d", kv_dtype);
     QR_CHECK_ARG(max_batch >= 1, "max_batch must be >= 1 (got %d)", max_batch);

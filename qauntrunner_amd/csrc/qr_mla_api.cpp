@@ -13,6 +13,7 @@ using namespace qr;
 struct qr_mla {
     int device = 0;
     int layers = 0, kv_lora = 0, rope = 0, latent = 0, max_seq = 0, dtype = 0;
+    bool split_set = true;  // false until qr_mla_set_rope for caches made by qr_mla_create_latent
     PagedStore store;
     int seq_len = 0;
     hipStream_t stream = nullptr;
@@ -123,6 +124,7 @@ int attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nope, int 
 }
 
 int validate_attention(const qr_mla* m, int layer, int pos, int heads) {
+    QR_CHECK_ARG(m->split_set, "the latent's kv_lora/rope split is not set (qr_mla_set_rope)");
     QR_TRY(check_layer(m, layer));
     QR_TRY(check_pos(m, pos));
     QR_TRY(check_resident(m, layer, pos));
@@ -133,6 +135,39 @@ int validate_attention(const qr_mla* m, int layer, int pos, int heads) {
 }  // namespace
 
 extern "C" {
+
+int qr_mla_create_latent(qr_mla** out, int layers, int latent_dim, int max_seq, int dtype) {
+    clear_error();
+    QR_CHECK_ARG(out != nullptr, "null output handle pointer");
+    *out = nullptr;
+    QR_CHECK_ARG(latent_dim >= 1 && latent_dim <= kMlaMaxLora + kMlaMaxRope, "latent_dim %d outside [1, %d]",
+                 latent_dim, kMlaMaxLora + kMlaMaxRope);
+    // storage needs the row width only; the split is fixed by qr_mla_set_rope
+    const int kv_lora = std::min(latent_dim, kMlaMaxLora);
+    const int st = qr_mla_create(out, layers, kv_lora, latent_dim - kv_lora, max_seq, dtype);
+    if (st == QR_OK) (*out)->split_set = false;
+    return st;
+}
+
+int qr_mla_set_rope(qr_mla* m, int rope) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(rope >= 0 && rope <= kMlaMaxRope && rope < m->latent && m->latent - rope <= kMlaMaxLora,
+                 "rope %d does not split a latent of %d into kv_lora <= %d and rope <= %d", rope, m->latent,
+                 kMlaMaxLora, kMlaMaxRope);
+    m->rope = rope;
+    m->kv_lora = m->latent - rope;
+    m->split_set = true;
+    return QR_OK;
+}
+
+int qr_mla_max_seq(const qr_mla* m, int* out) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(out, "null output pointer");
+    *out = m->max_seq;
+    return QR_OK;
+}
 
 int qr_mla_create(qr_mla** out, int layers, int kv_lora, int rope, int max_seq, int dtype) {
     clear_error();

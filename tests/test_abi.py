@@ -36,7 +36,9 @@ def test_version_and_status_names():
 @pytest.mark.parametrize("args,needle", [
     ((0, 8, 2, 64, 512, 0, 1), "layers"),
     ((1, 2, 4, 64, 512, 0, 1), "kv_heads"),
-    ((1, 8, 2, 48, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 44, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 8, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 264, 512, 0, 1), "head_dim"),
     ((1, 8, 2, 64, 0, 0, 1), "max_seq"),
     ((1, 8, 2, 64, 512, 7, 1), "dtype"),
     ((1, 8, 2, 64, 512, 0, 0), "max_batch"),
@@ -57,19 +59,28 @@ def test_mla_create_validates_before_device(args):
     assert L.qr_mla_create(ctypes.byref(h), *args) == _lib.QR_ERR_INVALID_ARGUMENT and not h.value
 
 
+@pytest.mark.parametrize("latent", [0, 1281, -5])
+def test_mla_create_latent_validates_before_device(latent):
+    L = qr.load()
+    h = ctypes.c_void_p()
+    assert L.qr_mla_create_latent(ctypes.byref(h), 1, latent, 100, 2) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert not h.value and "latent_dim" in L.qr_last_error().decode()
+
+
 def test_null_handles_are_rejected():
     L = qr.load()
     out = ctypes.c_int()
     assert L.qr_kv_seq_len(None, 0, ctypes.byref(out)) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_attention(None, 0, 0, 0, None, None, 1.0) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_mla_attention(None, 0, 0, 1, None, None, 1.0, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_set_rope(None, 64) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_destroy(None) == 0 and L.qr_mla_destroy(None) == 0
     assert "null" in L.qr_last_error().decode() or L.qr_last_error() == b""
 
 
 def test_status_maps_to_python_exceptions():
     with pytest.raises(qr.QrInvalidArgument):
-        qr.PagedKvCache(1, 8, 2, 48, 512)
+        qr.PagedKvCache(1, 8, 2, 44, 512)
     assert issubclass(qr.QrOutOfRange, IndexError) and issubclass(qr.QrNotResident, LookupError)
 
 

@@ -59,7 +59,7 @@ def test_mla_fixture_on_gpu(gpu):
 
     z = np.load(os.path.join(HERE, "mla_small.npz"))
     heads, lora, rope, seq = (int(x) for x in z["shape"])
-    with qr.MlaLatentCache(1, lora, rope, seq) as m:
+    with qr.MlaLatentCache(1, lora + rope, seq, rope=rope) as m:
         m.AppendRange(0, 0, z["lat"])
         got = m.AbsorbedAttention(0, seq - 1, z["q_tilde"], z["q_rope"], float(z["scale"]))
     assert_close(got, z["u"], 1e-3, 1e-4, "MLA fixture (fp32 latents)")

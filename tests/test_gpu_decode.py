@@ -129,6 +129,46 @@ def test_decode_16bit_mfma_shapes(gpu, dtype, heads, kv_heads, D, seq):
                          f"{dtype} H{heads}/Hkv{kv_heads}/D{D}/pos{p}")
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,D,seq", [
+    (32, 8, 80, 1500),   # 10 chunks of 8 per row, rounded up to 16 lanes
+    (16, 4, 96, 2049),
+    (8, 2, 120, 700),
+    (12, 4, 40, 513),
+    (4, 1, 200, 300),    # 25 chunks, rounded up to 32 lanes
+    (6, 3, 24, 777),
+    (5, 5, 136, 256),    # one query head per kv head, exactly one page
+])
+def test_decode_head_dims_not_a_power_of_two(gpu, dtype, heads, kv_heads, D, seq):
+    """PagedKvCache takes any headDim (PagedKvCache.cs:29-37); multiples of 8 that are not
+    powers of two run on the streaming kernel with the row's last lanes masked.  Rows past
+    the attended position hold NaN, so a masked lane that read a neighbour would show."""
+    q = normal(seq + 40, heads * D)
+    Kb, K = to_dtype_bits(normal(seq + 41, (seq, kv_heads * D)), dtype)
+    Vb, V = to_dtype_bits(normal(seq + 42, (seq, kv_heads * D)), dtype)
+    if dtype == "f32":
+        nanb = np.full((64, kv_heads * D), np.nan, np.float32)
+    else:  # quiet NaN bit patterns
+        nanb = np.full((64, kv_heads * D), 0x7E00 if dtype == "f16" else 0x7FC0, np.uint16)
+    scale = 1 / math.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, seq + 64, kv_dtype=dtype) as kv:
+        kv.AppendRange(0, 0, Kb, Vb, src_dtype=dtype)
+        kv.AppendRange(0, seq, nanb, nanb, src_dtype=dtype)
+        kr, vr = kv.Read(0, 0, seq)
+        assert np.array_equal(kr, Kb) and np.array_equal(vr, Vb)
+        check_decode(kv.Attention(0, seq - 1, q, scale), K, V, q, heads, kv_heads, D, scale,
+                     f"{dtype} H{heads}/Hkv{kv_heads}/D{D}/seq{seq}")
+        p = seq // 3
+        check_decode(kv.Attention(0, p, q, scale), K[:p + 1], V[:p + 1], q, heads, kv_heads, D, scale,
+                     f"{dtype} H{heads}/Hkv{kv_heads}/D{D}/pos{p}")
+        if dtype != "f32":  # causal queries over the same pages (the per-query fallback path)
+            qs = normal(seq + 43, (3, heads * D))
+            out = kv.AttentionChunk(0, seq - 3, qs, scale)
+            for i in range(3):
+                check_decode(out[i], K[:seq - 2 + i], V[:seq - 2 + i], qs[i], heads, kv_heads, D, scale,
+                             f"{dtype} D{D} chunk query {i}")
+
+
 @pytest.mark.parametrize("dtype,D", [("f32", 128), ("f16", 128), ("bf16", 64), ("f16", 32)])
 def test_stale_nan_rows_past_the_position_are_ignored(gpu, dtype, D):
     """Rows past the attended position that still hold NaN (an earlier sequence,

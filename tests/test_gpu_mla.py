@@ -33,7 +33,7 @@ def run_mla(dtype, heads, kv_lora, rope, n, pos=None, seed=0, layers=1, layer=0)
     qt = normal(seed + 1, (heads, kv_lora))
     qrp = normal(seed + 2, (heads, rope)) if rope else np.zeros((heads, 0), np.float32)
     scale = 1 / math.sqrt(192)
-    with qr.MlaLatentCache(layers, kv_lora, rope, n, dtype=dtype) as m:
+    with qr.MlaLatentCache(layers, kv_lora + rope, n, dtype=dtype, rope=rope) as m:
         m.AppendRange(layer, 0, bits, src_dtype=dtype)
         p = n - 1 if pos is None else pos
         got = m.AbsorbedAttention(layer, p, qt, qrp, scale)
@@ -80,7 +80,7 @@ def test_mla_absorbed_equals_expanded_through_gpu(gpu, rope):
     scale = 1 / math.sqrt(nope + rope)
     qt = oracle.mla_q_absorb(q, kvb, heads, nope, rope, vdim, kv_lora)
     qrp = q.reshape(heads, nope + rope)[:, nope:]
-    with qr.MlaLatentCache(1, kv_lora, rope, 64) as m:
+    with qr.MlaLatentCache(1, kv_lora + rope, 64, rope=rope) as m:
         for t in range(seq):
             m.Append(0, t, lat[t])
         u = m.AbsorbedAttention(0, seq - 1, qt, qrp, scale)
@@ -89,12 +89,35 @@ def test_mla_absorbed_equals_expanded_through_gpu(gpu, rope):
     assert np.max(np.abs(out - want)) <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_mla_reference_constructor_and_late_split(gpu, dtype):
+    """new MlaLatentCache(layers, latentDim, maxSeq) as StreamingEngine.cs:96-97 calls it:
+    appends need the row width only; attention needs the kv_lora/rope split, which MlaLayer
+    supplies (SetRope); the result equals a cache created with the split."""
+    kv_lora, rope, n, heads = 512, 64, 700, 16
+    lat = normal(31, (n, kv_lora + rope))
+    bits, _ = to_dtype_bits(lat, dtype)
+    qt, qrp = normal(32, (heads, kv_lora)), normal(33, (heads, rope))
+    with qr.MlaLatentCache(1, kv_lora + rope, 1000, dtype=dtype) as m, \
+            qr.MlaLatentCache(1, kv_lora + rope, 1000, dtype=dtype, rope=rope) as ref:
+        assert m.max_seq() == 1000
+        m.AppendRange(0, 0, bits, src_dtype=dtype)
+        ref.AppendRange(0, 0, bits, src_dtype=dtype)
+        with pytest.raises(qr.QrInvalidArgument):
+            m.AbsorbedAttention(0, n - 1, qt, qrp, 0.07)
+        with pytest.raises(qr.QrInvalidArgument):
+            m.SetRope(kv_lora + rope)              # no room for kv_lora
+        m.SetRope(rope)
+        assert np.array_equal(m.AbsorbedAttention(0, n - 1, qt, qrp, 0.07),
+                              ref.AbsorbedAttention(0, n - 1, qt, qrp, 0.07))
+
+
 def test_mla_cache_state(gpu):
     """Paging, Page() copy-out, BytesUsed, Truncate/Reset (MlaLatentCache.cs:29-65)."""
     kv_lora, rope, n = 512, 64, 600
     lat = normal(5, (n, kv_lora + rope))
     bits = oracle.f32_to_bf16(lat)
-    with qr.MlaLatentCache(2, kv_lora, rope, 1024, dtype="bf16") as m:
+    with qr.MlaLatentCache(2, kv_lora + rope, 1024, dtype="bf16", rope=rope) as m:
         for t in range(300):
             m.Append(1, t, lat[t])          # fp32 rows through the reference codec
         m.AppendRange(1, 300, bits[300:], src_dtype="bf16")
@@ -125,7 +148,7 @@ def test_mla_rows_past_pos_are_not_read_into_the_result(gpu):
     bits[pos + 1:] = 0x7FC0  # bf16 quiet NaN
     qt, qrp = normal(78, (heads, 512)), normal(79, (heads, 64))
     scale = 1 / math.sqrt(192)
-    with qr.MlaLatentCache(1, 512, 64, n, dtype="bf16") as m:
+    with qr.MlaLatentCache(1, 576, n, dtype="bf16", rope=64) as m:
         m.AppendRange(0, 0, bits, src_dtype="bf16")
         got = m.AbsorbedAttention(0, pos, qt, qrp, scale)
     assert np.isfinite(got).all()
@@ -146,7 +169,7 @@ def test_mla_dev_entry_with_unaligned_queries(gpu):
     qt_buf[1:] = torch.from_numpy(qt.ravel()).to(dev)
     qr_buf[3:] = torch.from_numpy(qrp.ravel()).to(dev)
     u = torch.empty(heads * 512, dtype=torch.float32, device=dev)
-    with qr.MlaLatentCache(1, 512, 64, n, dtype="bf16") as m:
+    with qr.MlaLatentCache(1, 576, n, dtype="bf16", rope=64) as m:
         m.AppendRange(0, 0, bits, src_dtype="bf16")
         m.AbsorbedAttentionDev(0, n - 1, qt_buf[1:], qr_buf[3:], u, scale)
         torch.cuda.synchronize()
@@ -187,7 +210,7 @@ def test_mla_bf16_latents_outside_the_fp16_range(gpu, case):
         qrp *= 1e6
     bits, latd = to_dtype_bits(lat, "bf16")
     scale = 1 / math.sqrt(192)
-    with qr.MlaLatentCache(1, kv_lora, rope, n, dtype="bf16") as m:
+    with qr.MlaLatentCache(1, kv_lora + rope, n, dtype="bf16", rope=rope) as m:
         m.AppendRange(0, 0, bits, src_dtype="bf16")
         got = m.AbsorbedAttention(0, n - 1, qt, qrp, scale)
     want = oracle.mla_attention(latd, qt, qrp, kv_lora, rope, scale)

@@ -135,7 +135,7 @@ def test_attend_absorbed_layer(gpu, dtype, fmt, heads, rope, n, pos):
     want = _layer_oracle(latd, w, q, heads, nope, rope, vdim, kv_lora, p)
     code = quant.FMT[fmt]
     tol = 1e-4 if dtype == "f32" else 5e-3
-    with qr.MlaLatentCache(1, kv_lora, rope, n, dtype=dtype) as m:
+    with qr.MlaLatentCache(1, kv_lora + rope, n, dtype=dtype, rope=rope) as m:
         m.AppendRange(0, 0, bits, src_dtype=dtype)
         W = qr.Weight(code, heads * (nope + vdim), kv_lora, raw)
         got = m.AttendAbsorbed(0, p, q, W, nope, vdim)
@@ -156,7 +156,7 @@ def test_attend_absorbed_equals_expanded(gpu):
     R = lambda *s: (rng.random(s) * 2 - 1).astype(np.float32)  # noqa: E731
     q, kvb, lat = R(heads, nope + rope), R(heads * (nope + vdim), kv_lora), R(seq, kv_lora + rope)
     scale = 1 / math.sqrt(nope + rope)
-    with qr.MlaLatentCache(1, kv_lora, rope, 64) as m:
+    with qr.MlaLatentCache(1, kv_lora + rope, 64, rope=rope) as m:
         m.AppendRange(0, 0, lat)
         W = qr.Weight("F32", heads * (nope + vdim), kv_lora, kvb.view(np.uint8))
         got = m.AttendAbsorbed(0, seq - 1, q, W, nope, vdim)
@@ -167,7 +167,7 @@ def test_attend_absorbed_equals_expanded(gpu):
 
 def test_attend_absorbed_errors(gpu):
     kv_lora, rope = 64, 16
-    with qr.MlaLatentCache(1, kv_lora, rope, 300) as m:
+    with qr.MlaLatentCache(1, kv_lora + rope, 300, rope=rope) as m:
         m.AppendRange(0, 0, normal(3, (10, kv_lora + rope)))
         raw, _ = kvb_rows("F16", 4, 8, 8, kv_lora, 2)
         W = qr.Weight("F16", 4 * 16, kv_lora, raw)

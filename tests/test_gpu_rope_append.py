@@ -94,7 +94,8 @@ def test_rope_append_dev_bulk(gpu, dtype):
     assert same >= 0.99
 
 
-@pytest.mark.parametrize("dtype,D", [("f16", 128), ("bf16", 128), ("f16", 64), ("bf16", 64)])
+@pytest.mark.parametrize("dtype,D", [("f16", 128), ("bf16", 128), ("f16", 64), ("bf16", 64), ("f16", 80),
+                                     ("bf16", 96)])
 def test_rope_append_dev_ragged_ranges(gpu, dtype, D):
     """Device appends at unaligned positions and lengths (single rows, runs that end
     mid-chunk, runs across page boundaries): every V row read back equals its 16-bit
