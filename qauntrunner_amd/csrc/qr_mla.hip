@@ -144,19 +144,27 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // ---------------------------------------------------------------------------
 // MFMA path for 16-bit latents (kv_lora 512, rope 0 or 64).
 //
-// Workgroup = 4 waves = 32 heads over one split of the sequence, walked in tiles
-// of 64 positions.  A tile (64 latent rows, contiguous inside one page) is copied
-// into LDS by the LDS-DMA path (global_load_lds_dwordx4), into one of two
-// buffers, so the copy of tile t+1 runs under the MFMAs of tile t.
-//   QK  wave w scores positions 32(w/2)..32(w/2)+31 of the tile for heads
+// Workgroup = 8 waves (two per SIMD) = 32 heads over one split of the sequence,
+// walked in tiles of 32 positions.  Waves 0-3 compute scores, waves 4-7 the softmax
+// and PV, so on every SIMD one wave's MFMAs run beside the other's softmax and loads.
+// A tile (32 latent rows, contiguous inside one page) is loaded into registers of
+// the PV waves two tiles ahead of its use and written to one of three LDS buffers.
+//   QK  wave w < 4 scores positions 16(w/2)..16(w/2)+15 of the tile for heads
 //       16(w%2)..16(w%2)+15: S^T[pos][head] = C[pos][dims] . q~^T[dims][head]; A is
 //       read from the row-major tile, B = the wave's 16 heads of q~ (hi + lo) stays in
-//       registers.
-//   The scores go through LDS so that every wave sees all 64 positions; every
-//   wave runs the same online softmax (log2 units) and so holds the same (m, l).
-//   PV  wave w owns latent dims 128w..128w+127 for all 32 heads:
+//       registers.  Raw scores go to LDS.
+//   Softmax (log2 units, online): PV wave v owns heads 8v..8v+7; it keeps their (m, l)
+//   and writes P (hi + lo parts) and the accumulator rescale factor of each head to
+//   LDS.
+//   PV  wave 4 + v owns latent dims 128v..128v+127 for all 32 heads:
 //       U^T[dim][head] += C^T[dim][pos] . P^T[pos][head]; the C^T operand is read
 //       from the same row-major tile with ds_read_b64_tr_b16.
+// Two waves per SIMD because a single wave keeps too few LDS reads in flight: on
+// gfx950 one wave per SIMD reads ~100 bytes/clk per CU from LDS, two reach ~190.
+// Step t, two barriers: the QK waves score tile t+1 while the PV waves run the
+// softmax of tile t (scores written in step t-1); a barrier publishes P; the PV waves
+// accumulate tile t and store tile t+2 into LDS; the barrier that ends the step
+// publishes the scores of tile t+1 and tile t+2, and frees P and the buffer of tile t.
 // v_mfma_f32_16x16x32_f16 lane layout (checked on gfx950):
 //   A[m = lane%16][k = 8*(lane/16)+i], B[k = 8*(lane/16)+i][n = lane%16],
 //   D[m = 4*(lane/16)+r][n = lane%16].
@@ -164,7 +172,7 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 //   receives element i (0..3) from the 8 bytes addressed by lane 4i + j/4, at
 //   element j%4 of them.
 // In PV the 8 k-slots of lane quarter q are the positions {4q..4q+3, 16+4q..16+4q+3}
-// of a 32-position step, so each half of a transposed read touches 8 distinct rows.
+// of the tile, so each half of a transposed read touches 8 distinct rows.
 // Both products run in the cache's own 16-bit type, so the latent enters every MFMA
 // unconverted and any finite latent value is handled exactly.  QK: q~ is split into
 // hi + lo parts of that type (two MFMAs per k-step), keeping about 16 (bf16) or 22
@@ -175,15 +183,17 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // fp16 times a per-(head, split) power of two chosen from the largest |u_s| of the
 // head, so they neither overflow nor lose their small values whatever the latent's
 // range (a bf16 latent may hold values far outside fp16's range).
-// LDS tile layout: blocks of 8 logical 16-byte chunks (128 bytes) x 64 rows; inside
+// LDS tile layout: blocks of 8 logical 16-byte chunks (128 bytes) x 32 rows; inside
 // a block, chunk c of row r sits at slot (c % 8) ^ f(r), where f(r) is the 3-bit
 // reversal of (r >> 1) & 7, so the 16 rows of a QK read and the 8 rows of half a
 // transposed read fall on distinct banks.
-constexpr int kMTile = 64;                 // positions per tile
+constexpr int kMTile = 32;                 // positions per tile
 constexpr int kMHeads = 32;                // heads per workgroup
+constexpr int kMWaves = 8;
 constexpr int kMfmaLora = 512;
-constexpr int kScoreStride = kMTile + 4;   // floats per head row of the score buffer
+constexpr int kScoreStride = kMTile + 4;   // floats per head row of a score buffer
 constexpr float kRescaleSlack = 8.f;       // log2 units
+constexpr int kQkAhead = 4;                // QK k-steps whose A operands are read ahead
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_ptr;
@@ -191,6 +201,18 @@ typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_ptr;
 __device__ __forceinline__ int row_swizzle(int r) {
     const int x = (r >> 1) & 7;
     return ((x & 1) << 2) | (x & 2) | (x >> 2);
+}
+
+// max(x of this lane, x of lane ^ 16) / (lane ^ 32), the same value in both lanes:
+// v_permlane16_swap / v_permlane32_swap hand each lane the values of both lanes of
+// its pair (checked on gfx950: element 0 the lower lane's, element 1 the upper's).
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // MFMA operands in the cache's own 16-bit type.
@@ -224,19 +246,29 @@ struct MlaMK {
 };
 
 template <bool SRC_BF16, int KR>
-__global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
+__global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     constexpr int KL = kMfmaLora;
     constexpr int W = KL + KR;            // latent width (elements)
     constexpr int RB = W * 2;             // row bytes
-    constexpr int CR = W / 8;             // 16-byte chunks per row
     constexpr int NK = W / 32;            // QK k-steps
-    constexpr int TB = kMTile * RB;       // tile bytes = CR KiB
-    constexpr int DMA_PER_WAVE = CR / 4;  // 1 KiB DMA instructions per wave per tile
+    constexpr int NB = W / 64;            // 128-byte column blocks of a row
+    constexpr int BB = kMTile * 128;      // block bytes
+    constexpr int TB = NB * BB;           // tile bytes
+    constexpr int NLD = 4 * NB;           // 1 KiB wave loads per tile, all by the PV waves
+    constexpr int LDW = NLD / 4;          // loads per PV wave
+    constexpr int PR = kMTile * 2 + 16;   // bytes per head row of P (k-slot order, padded)
     using MT = PvType<SRC_BF16>;          // MFMA operands in the cache type
+    typedef typename MT::vec V;
+    typedef typename MT::elem E;
 
-    __shared__ __attribute__((aligned(1024))) char lds_t0[TB];
-    __shared__ __attribute__((aligned(1024))) char lds_t1[TB];
-    __shared__ __attribute__((aligned(16))) float lds_s[kMHeads * kScoreStride];
+    __shared__ __attribute__((aligned(1024))) char lds_b0[TB];
+    __shared__ __attribute__((aligned(1024))) char lds_b1[TB];
+    __shared__ __attribute__((aligned(1024))) char lds_b2[TB];
+    __shared__ __attribute__((aligned(16))) float lds_s0[kMHeads * kScoreStride];
+    __shared__ __attribute__((aligned(16))) float lds_s1[kMHeads * kScoreStride];
+    __shared__ __attribute__((aligned(16))) char lds_p[2 * kMHeads * PR];  // P hi rows, then lo rows
+    __shared__ float lds_corr[kMHeads];  // accumulator rescale factor of the tile
+    __shared__ float lds_l[kMHeads];
     __shared__ float lds_amax[4][kMHeads];
     __shared__ int lds_qexp[kMHeads];
 
@@ -253,19 +285,17 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
     const int ntiles = (t_end - t_begin + kMTile - 1) / kMTile;  // >= 1
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;  // wave-uniform (SGPR), 0..3
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & (kMWaves - 1);  // wave-uniform (SGPR)
+    const bool qk_wave = wave < 4;   // waves 0-3: QK; waves 4-7: softmax, PV and the tile copies
+    const int pw = wave & 3;         // index inside the role
     const int q4 = lane >> 4;
     const int l16 = lane & 15;
 
-    // LDS-DMA of the tile at t0 into buffer `dst`: instruction n fills bytes
-    // [1024n, 1024n + 1024), lane j the 16 bytes at 1024n + 16j, i.e. slot P = 64n + j
-    // = row P / CR, swizzled chunk P % CR.  Rows past the sequence end repeat the
-    // last valid row (finite data under a zero weight).
-    // Buffer-load DMA of one tile.  Block g of the LDS tile (8 KiB) holds logical
-    // chunks 8g..8g+7 of all 64 rows, 128 bytes per row; instruction (g, j) fills
-    // rows 8j..8j+7 of block g, lane L the row 8j + L/8, slot L%8, which holds chunk
-    // 8g + ((L%8) ^ f(row)).  Rows past the sequence end are outside the buffer
-    // range and read as zeros.
+    // Tile copy (PV waves).  Block g of the LDS tile (4 KiB) holds logical chunks
+    // 8g..8g+7 of all 32 rows, 128 bytes per row; load (g, j), j < 4, covers rows
+    // 8j..8j+7 of block g, lane L the row 8j + L/8, slot L%8, which holds chunk
+    // 8g + ((L%8) ^ f(row)).  Rows past the sequence end are outside the buffer range
+    // and read as zeros.
     const int drow = lane >> 3;
     int dma_voff[2];  // per parity of j: f(8j + L/8) = rev3(4 (j & 1) + L/16)
 #pragma unroll
@@ -274,42 +304,53 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
         const int f = ((x & 1) << 2) | (x & 2) | (x >> 2);
         dma_voff[jp] = drow * RB + 16 * ((lane & 7) ^ f);
     }
-    auto dma = [&](int t0, long long phys, char* dst) {
-        const char* base = p.pool + (phys * kPageTokens + (t0 & (kPageTokens - 1))) * RB;
+    auto page_of = [&](int t0) { return __builtin_amdgcn_readfirstlane(p.page_table[t0 >> kPageShift]); };
+    typedef U32x4 TileRegs[LDW];
+    auto load_tile = [&](int t0, int phys, TileRegs& r) __attribute__((always_inline)) {
+        const char* base = p.pool + (static_cast<long long>(phys) * kPageTokens + (t0 & (kPageTokens - 1))) * RB;
         const int bytes = min(kMTile, t_end - t0) * RB;
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, bytes, kBufferFlags);
 #pragma unroll
-        for (int i = 0; i < DMA_PER_WAVE; ++i) {
-            const int n = wave + 4 * i;  // wave-uniform
-            const int g = n >> 3, j = n & 7;
-            buffer_load_lds16(rsrc, dst + 8192 * g + 1024 * j, dma_voff[j & 1], 8 * j * RB + 128 * g);
+        for (int i = 0; i < LDW; ++i) {
+            const int n = pw + 4 * i;  // wave-uniform
+            const int g = n >> 2, j = n & 3;
+            r[i] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, dma_voff[j & 1], 8 * j * RB + 128 * g, 0));
         }
     };
-    dma(t_begin, p.page_table[t_begin >> kPageShift], lds_t0);
-    // page of the next tile to copy, loaded one tile ahead
-    int phys_next = ntiles > 1 ? p.page_table[(t_begin + kMTile) >> kPageShift] : 0;
+    auto store_tile = [&](const TileRegs& r, char* dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < LDW; ++i) {
+            const int n = pw + 4 * i;
+            const int g = n >> 2, j = n & 3;
+            *reinterpret_cast<U32x4*>(dst + BB * g + 1024 * j + 16 * lane) = r[i];
+        }
+    };
+    TileRegs tr0, tr1;  // tiles in flight (PV waves)
+    if (!qk_wave) {
+        load_tile(t_begin, page_of(t_begin), tr0);
+        if (ntiles > 1) load_tile(t_begin + kMTile, page_of(t_begin + kMTile), tr1);
+    }
 
-    // ---- B operands of QK: lane (q4, l16) holds dims 32kk + 8q4 .. +8 of head 16ht + l16
-    // (the wave's head tile ht = w % 2), split into hi + lo parts of the cache type (fp16:
-    // after the per-head power-of-two scaling).  q~ of the workgroup's 32 heads is read
-    // once, coalesced, converted to hi + lo and staged in tile buffer 1 (free until the
-    // second tile's copy), then every wave reads its 16 heads' operands from there.
-    const int ht = wave & 1;
-    const int ph = wave >> 1;  // position half of the tile
+    // ---- B operands of QK: lane (q4, l16) of QK wave (ph, ht) = (w / 2, w % 2) holds
+    // dims 32kk + 8q4 .. +8 of head 16ht + l16, split into hi + lo parts of the cache type
+    // (fp16: after the per-head power-of-two scaling).  q~ of the workgroup's 32 heads is
+    // read once, coalesced, converted to hi + lo and staged in tile buffers 1 (hi) and 2
+    // (lo), free until tiles 1 and 2 are stored; then every QK wave reads its operands.
     // staged rows of one part: W * 2 bytes, 16-byte chunk c of row r at chunk c ^ (r & 7)
     // (W / 8 is a multiple of 8), so the 16 rows of one operand read use distinct banks
     constexpr int QS = W * 2;
-    static_assert(2 * kMHeads * QS <= TB, "q~ hi + lo staging must fit in one tile buffer");
+    static_assert(kMHeads * QS == TB, "one part of q~ fills one tile buffer");
     {
-        // eight threads per head, thread `part` takes float4 columns part, part + 8, ...
-        const int hl = tid >> 3;
-        const int part = tid & 7;
+        // sixteen threads per head, thread `part` takes float4 columns part, part + 16, ...
+        constexpr int NQ = W / 64;
+        const int hl = tid >> 4;
+        const int part = tid & 15;
         const int head = min(hg * kMHeads + hl, p.heads - 1);  // padding heads are never stored
-        float4 v[NK];
+        float4 v[NQ];
         float amax = 0.f;
 #pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const int d = 4 * (part + 8 * i);
+        for (int i = 0; i < NQ; ++i) {
+            const int d = 4 * (part + 16 * i);
             v[i] = d < KL ? *reinterpret_cast<const float4*>(p.q_tilde + static_cast<size_t>(head) * KL + d)
                           : *reinterpret_cast<const float4*>(p.q_rope + static_cast<size_t>(head) * KR + (d - KL));
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
@@ -319,11 +360,11 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
             amax = fmaxf(amax, dpp_xor1(amax));
             amax = fmaxf(amax, dpp_xor2(amax));
             amax = fmaxf(amax, dpp_half_mirror(amax));
+            amax = fmaxf(amax, dpp_mirror(amax));
             if (amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
         }
-        typedef typename MT::elem E;
 #pragma unroll
-        for (int i = 0; i < NK; ++i) {
+        for (int i = 0; i < NQ; ++i) {
             const float x[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
             E hi[4], lo[4];
 #pragma unroll
@@ -332,195 +373,235 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
                 hi[c] = static_cast<E>(y);
                 lo[c] = static_cast<E>(y - static_cast<float>(hi[c]));
             }
-            const int col = part + 8 * i;  // 8-byte column: chunk col / 2, half col % 2
-            char* row = lds_t1 + hl * QS + 16 * ((col >> 1) ^ (hl & 7)) + 8 * (col & 1);
-            *reinterpret_cast<uint2*>(row) = __builtin_bit_cast(uint2, hi);
-            *reinterpret_cast<uint2*>(row + kMHeads * QS) = __builtin_bit_cast(uint2, lo);
+            const int col = part + 16 * i;  // 8-byte column: chunk col / 2, half col % 2
+            const int off = hl * QS + 16 * ((col >> 1) ^ (hl & 7)) + 8 * (col & 1);
+            *reinterpret_cast<uint2*>(lds_b1 + off) = __builtin_bit_cast(uint2, hi);
+            *reinterpret_cast<uint2*>(lds_b2 + off) = __builtin_bit_cast(uint2, lo);
         }
         if (part == 0) lds_qexp[hl] = qexp;
     }
-    lds_barrier();
-    typename MT::vec qhi[NK], qlo[NK];
-    float sscale;
-    {
-        const int hr = 16 * ht + l16;
+    if (!qk_wave) store_tile(tr0, lds_b0);
+    lds_barrier();  // q~ staged, tile 0 in LDS
+
+    // ================================================================ QK waves
+    if (qk_wave) {
+        const int ht = wave & 1;   // head tile
+        const int ph = wave >> 1;  // position half of the tile
+        V qhi[NK], qlo[NK];
+        {
+            const int hr = 16 * ht + l16;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-            const int c = (4 * kk + q4) ^ (hr & 7);
-            qhi[kk] = *reinterpret_cast<const typename MT::vec*>(lds_t1 + hr * QS + 16 * c);
-            qlo[kk] = *reinterpret_cast<const typename MT::vec*>(lds_t1 + (kMHeads + hr) * QS + 16 * c);
+            for (int kk = 0; kk < NK; ++kk) {
+                const int c = (4 * kk + q4) ^ (hr & 7);
+                qhi[kk] = *reinterpret_cast<const V*>(lds_b1 + hr * QS + 16 * c);
+                qlo[kk] = *reinterpret_cast<const V*>(lds_b2 + hr * QS + 16 * c);
+            }
         }
-        sscale = p.qscale * ldexpf(1.f, lds_qexp[hr]);
+        // A operand: row 16ph + l16, logical chunk 4kk + q4 = block kk/2, slot
+        // 4 (kk & 1) + q4, stored at slot (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) +
+        // (q4 ^ (f & 3)); f depends on l16 only (16ph is a multiple of 16).
+        const int rq = 16 * ph + l16;
+        const int fq = row_swizzle(rq);
+        const int qk_off = rq * 128 + 16 * (q4 ^ (fq & 3));
+        const int qk_flip = fq >> 2;
+        // raw scores of the tile in `tile` into `sbuf` (the softmax scales and masks)
+        auto qk = [&](const char* tile, float* sbuf) __attribute__((always_inline)) {
+            f32x4_t sc[2], sl[2];  // hi / lo chains x parity of the k-step
+#pragma unroll
+            for (int e = 0; e < 2; ++e) sc[e] = sl[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            U32x4 ra[NK];
+            auto load = [&](int kk) __attribute__((always_inline)) {
+                ra[kk] = *reinterpret_cast<const U32x4*>(tile + BB * (kk >> 1) + qk_off + 64 * ((kk & 1) ^ qk_flip));
+            };
+#pragma unroll
+            for (int kk = 0; kk < kQkAhead; ++kk) load(kk);
+#pragma unroll
+            for (int kk = 0; kk < NK; ++kk) {
+                if (kk + kQkAhead < NK) load(kk + kQkAhead);
+                const V av = __builtin_bit_cast(V, ra[kk]);
+                sc[kk & 1] = MT::mma(av, qhi[kk], sc[kk & 1]);
+                sl[kk & 1] = MT::mma(av, qlo[kk], sl[kk & 1]);
+            }
+            // lane holds positions 16ph + 4q4 + r of head 16ht + l16
+            *reinterpret_cast<f32x4_t*>(sbuf + (16 * ht + l16) * kScoreStride + 16 * ph + 4 * q4) =
+                (sc[0] + sc[1]) + (sl[0] + sl[1]);
+        };
+        qk(lds_b0, lds_s0);
+        lds_barrier();  // q~ read by every QK wave: buffer 1 may be refilled
+        lds_barrier();  // scores of tile 0 published, tile 1 in LDS
+        // step t: QK of tile t+1 while the PV waves run the softmax of tile t
+        for (int t = 0;; t += 6) {
+#define QR_QK_STEP(T, NXT, SN)                                   \
+            if ((T) + 1 < ntiles) qk(NXT, SN);                   \
+            lds_barrier();                                       \
+            lds_barrier();                                       \
+            if ((T) + 1 >= ntiles) break;
+            QR_QK_STEP(t, lds_b1, lds_s1)
+            QR_QK_STEP(t + 1, lds_b2, lds_s0)
+            QR_QK_STEP(t + 2, lds_b0, lds_s1)
+            QR_QK_STEP(t + 3, lds_b1, lds_s0)
+            QR_QK_STEP(t + 4, lds_b2, lds_s1)
+            QR_QK_STEP(t + 5, lds_b0, lds_s0)
+#undef QR_QK_STEP
+        }
+        lds_barrier();  // l published
+        lds_barrier();  // amax published
+        lds_barrier();  // partial rows staged
+        return;
     }
 
-    // Per-lane LDS offsets (layout of the DMA above).  QK: rows 32ph + 16mt + l16,
-    // logical chunk 4kk + q4 = block kk/2, slot 4 (kk & 1) + q4, stored at slot
-    // (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) + (q4 ^ (f & 3)); f depends on
-    // l16 only (32ph + 16mt is a multiple of 16).
-    const int rq = 32 * ph + l16;
-    const int fq = row_swizzle(rq);
-    const int qk_off = rq * 128 + 16 * (q4 ^ (fq & 3));
-    const int qk_flip = fq >> 2;
-    // PV: half h of the A operand of dim tile dt, step ks reads row
-    // 32ks + 16h + 4q4 + l16/4, dims 128w + 16dt + 4(l16 & 3) .. +4: logical chunk
-    // 16w + 2dt + ((l16 & 3) >> 1) = block 2w + dt/4, slot 2 (dt & 3) + ((l16 & 3) >> 1),
-    // byte 8 (l16 & 1).  f of that row depends on 4q4 + l16/4 only.
+    // ================================================================ PV waves
+    // softmax: PV wave pw owns heads 8pw..8pw+7; lane (lane / 8, i8) holds positions
+    // 4 i8 .. 4 i8 + 3 of head hs
+    const int hs = 8 * pw + (lane >> 3);
+    const int i8 = lane & 7;
+    const float sscale = p.qscale * ldexpf(1.f, lds_qexp[hs]);
+    float m_s = -INFINITY, l_s = 0.f;  // running max and sum of head hs
+    // k-slot of position 4 i8 in the P^T operand order (slots 8q + i: positions 4q + i
+    // for i < 4, 16 + 4q + i - 4 otherwise); positions 4 i8 + 1..3 follow it
+    const int pslot = i8 < 4 ? 8 * i8 : 8 * (i8 - 4) + 4;
+    // PV: half h of the A operand of dim tile dt reads row 16h + 4q4 + l16/4, dims
+    // 128pw + 16dt + 4(l16 & 3) .. +4: logical chunk 16pw + 2dt + ((l16 & 3) >> 1) =
+    // block 2pw + dt/4, slot 2 (dt & 3) + ((l16 & 3) >> 1), byte 8 (l16 & 1).  f of that
+    // row depends on 4q4 + l16/4 only.
     const int rp = 4 * q4 + (l16 >> 2);
     const int fp = row_swizzle(rp);
     const int a4 = l16 & 3;
-    const int pv_off = 16384 * wave + rp * 128 + 16 * ((a4 >> 1) ^ (fp & 1)) + 8 * (a4 & 1);
+    const int pv_off = 2 * BB * pw + rp * 128 + 16 * ((a4 >> 1) ^ (fp & 1)) + 8 * (a4 & 1);
     int pv_dt[4];  // slot pair of dt & 3: 2 ((dt & 3) ^ (f >> 1)) chunks
 #pragma unroll
     for (int x = 0; x < 4; ++x) pv_dt[x] = 32 * (x ^ (fp >> 1));
+
+    lds_barrier();  // q~ read by every QK wave: buffer 1 may be refilled
+    if (ntiles > 1) store_tile(tr1, lds_b1);
+    int phys_next = ntiles > 2 ? page_of(t_begin + 2 * kMTile) : 0;
+    lds_barrier();  // scores of tile 0 published, tile 1 in LDS
 
     f32x4_t acc[2][8];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[nt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m[2] = {-INFINITY, -INFINITY};
-    float l[2] = {0.f, 0.f};
 
-    // One tile; `tile` and `next` are always the two distinct buffers by name, so
-    // the compiler can tell the LDS reads of `tile` from the DMA into `next` and
-    // does not wait for that DMA before reading.
-    auto step = [&](int it, const char* tile, char* next) __attribute__((always_inline)) {
-        const int t0 = t_begin + it * kMTile;
-        wait_dma();
-        lds_barrier();  // tile `it` is in LDS; tile it-1 (or the staged q~), its scores are consumed
-        if (it + 1 < ntiles) dma(t0 + kMTile, __builtin_amdgcn_readfirstlane(phys_next), next);
-        if (it + 2 < ntiles) phys_next = p.page_table[(t0 + 2 * kMTile) >> kPageShift];
+    // Step t: tile t in `cur` with its raw scores in `s_cur`; tile t+2 is loaded now
+    // and stored into `dst` (the buffer of tile t-1) after the barrier that publishes P.
+    auto step = [&](int t, const char* cur, char* dst, const float* s_cur) __attribute__((always_inline)) {
+        const int t0 = t_begin + t * kMTile;
+        const bool copy = t + 2 < ntiles;
+        if (copy) load_tile(t0 + 2 * kMTile, phys_next, tr0);
+        if (t + 3 < ntiles) phys_next = page_of(t0 + 3 * kMTile);
 
-        // ---- QK: M tiles mt = positions 32ph + 16mt .. +16, one N tile of 16 heads
-        // hi and lo products go to separate accumulators: four independent MFMA chains
-        f32x4_t sc[2], sl[2];
+        // ---- softmax of tile t for head hs (only the last tile can be partial)
+        {
+            const float4 r = *reinterpret_cast<const float4*>(s_cur + hs * kScoreStride + 4 * i8);
+            float v[4] = {r.x * sscale, r.y * sscale, r.z * sscale, r.w * sscale};
+            if (t0 + kMTile > t_end) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) sc[mt] = sl[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk)
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const U32x4 raw = *reinterpret_cast<const U32x4*>(tile + 8192 * (kk >> 1) + 2048 * mt + qk_off +
-                                                                  64 * ((kk & 1) ^ qk_flip));
-                const auto av = __builtin_bit_cast(typename MT::vec, raw);
-                sc[mt] = MT::mma(av, qhi[kk], sc[mt]);
-                sl[mt] = MT::mma(av, qlo[kk], sl[mt]);
+                for (int i = 0; i < 4; ++i)
+                    if (t0 + 4 * i8 + i >= t_end) v[i] = -INFINITY;
             }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) sc[mt] += sl[mt];
-        // lane holds positions 32ph + 16mt + 4q4 + r of head 16ht + l16
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            float4 s4;
-            const int pos = t0 + 32 * ph + 16 * mt + 4 * q4;
-            s4.x = pos + 0 < t_end ? sc[mt][0] * sscale : -INFINITY;
-            s4.y = pos + 1 < t_end ? sc[mt][1] * sscale : -INFINITY;
-            s4.z = pos + 2 < t_end ? sc[mt][2] * sscale : -INFINITY;
-            s4.w = pos + 3 < t_end ? sc[mt][3] * sscale : -INFINITY;
-            *reinterpret_cast<float4*>(lds_s + (16 * ht + l16) * kScoreStride + 32 * ph + 16 * mt + 4 * q4) = s4;
-        }
-        lds_barrier_dma_in_flight();
-
-        // ---- softmax over the 64 positions; P^T operands: k-slot 8q4 + i of step ks
-        // is position 32ks + 4q4 + i (i < 4) or 32ks + 16 + 4q4 + i - 4
-        using PV = MT;
-        typename PV::vec pb[2][2], pl[2][2];  // P as hi + lo parts of the cache type
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            float s[2][8];
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const float* row = lds_s + (16 * nt + l16) * kScoreStride + 32 * ks + 4 * q4;
-                const float4 x = *reinterpret_cast<const float4*>(row);
-                const float4 y = *reinterpret_cast<const float4*>(row + 16);
-                s[ks][0] = x.x; s[ks][1] = x.y; s[ks][2] = x.z; s[ks][3] = x.w;
-                s[ks][4] = y.x; s[ks][5] = y.y; s[ks][6] = y.z; s[ks][7] = y.w;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) tmax = fmaxf(tmax, s[ks][i]);
-            }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            float tmax = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+            tmax = fmaxf(tmax, dpp_xor1(tmax));
+            tmax = fmaxf(tmax, dpp_xor2(tmax));
+            tmax = fmaxf(tmax, dpp_half_mirror(tmax));  // the same in the 8 lanes of the head
             // Lazy rescale: the reference m moves only when the tile max exceeds it by
             // more than 2^8, so P = 2^(s - m) <= 256 and the accumulators are rescaled
-            // in few tiles (skipped by the whole wave when no lane needs it).
-            const bool grow = tmax > m[nt] + kRescaleSlack;
-            const bool rescale = grow && m[nt] != -INFINITY;
-            if (__builtin_amdgcn_ballot_w64(rescale)) {
-                const float corr = rescale ? fast_exp2(m[nt] - tmax) : 1.f;
-                l[nt] *= corr;
+            // in few tiles.
+            const bool grow = tmax > m_s + kRescaleSlack;
+            const float corr = grow && m_s != -INFINITY ? fast_exp2(m_s - tmax) : 1.f;
+            if (grow) m_s = tmax;
+            const float mref = m_s == -INFINITY ? 0.f : m_s;  // masked-only so far: weights 0, not NaN
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = fast_exp2(v[i] - mref);
+            l_s = l_s * corr + group_sum((e[0] + e[1]) + (e[2] + e[3]), 8);
+            typedef E E4 __attribute__((ext_vector_type(4)));
+            E4 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hi[i] = static_cast<E>(e[i]);
+                lo[i] = static_cast<E>(e[i] - static_cast<float>(hi[i]));
+            }
+            *reinterpret_cast<E4*>(lds_p + hs * PR + 2 * pslot) = hi;
+            *reinterpret_cast<E4*>(lds_p + (kMHeads + hs) * PR + 2 * pslot) = lo;
+            if (i8 == 0) lds_corr[hs] = corr;
+        }
+        lds_barrier();  // P and the rescale factors of tile t are published
+
+        // ---- PV of tile t over this wave's 128 dims, P^T of heads 16nt + l16 from LDS
+        V pb[2], pl[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            pb[nt] = *reinterpret_cast<const V*>(lds_p + (16 * nt + l16) * PR + 16 * q4);
+            pl[nt] = *reinterpret_cast<const V*>(lds_p + (kMHeads + 16 * nt + l16) * PR + 16 * q4);
+            const float corr = lds_corr[16 * nt + l16];
+            if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) acc[nt][dt] *= corr;
             }
-            if (grow) m[nt] = tmax;
-            const float mref = m[nt] == -INFINITY ? 0.f : m[nt];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float e = fast_exp2(s[ks][i] - mref);
-                    l[nt] += e;
-                    const typename PV::elem hi = static_cast<typename PV::elem>(e);
-                    pb[nt][ks][i] = hi;
-                    pl[nt][ks][i] = static_cast<typename PV::elem>(e - static_cast<float>(hi));
-                }
         }
-
-        // ---- PV over this wave's 128 dims
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const char* a0 = tile + pv_off + 8192 * (dt >> 2) + 4096 * ks + pv_dt[dt & 3];
-                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4_ptr)(a0));
-                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4_ptr)(a0 + 2048));
-                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                const u32x2_t lw = __builtin_bit_cast(u32x2_t, lo);
-                const u32x2_t hw = __builtin_bit_cast(u32x2_t, hi);
-                typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-                const auto av = __builtin_bit_cast(typename PV::vec, u32x4_t{lw.x, lw.y, hw.x, hw.y});
-                acc[0][dt] = PV::mma(av, pb[0][ks], acc[0][dt]);
-                acc[0][dt] = PV::mma(av, pl[0][ks], acc[0][dt]);
-                acc[1][dt] = PV::mma(av, pb[1][ks], acc[1][dt]);
-                acc[1][dt] = PV::mma(av, pl[1][ks], acc[1][dt]);
-            }
+        for (int dt = 0; dt < 8; ++dt) {
+            const char* a0 = cur + pv_off + BB * (dt >> 2) + pv_dt[dt & 3];
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            const u32x2_t lw = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(a0)));
+            const u32x2_t hw = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr)(a0 + 16 * 128)));
+            const V av = __builtin_bit_cast(V, u32x4_t{lw.x, lw.y, hw.x, hw.y});
+            acc[0][dt] = MT::mma(av, pb[0], acc[0][dt]);
+            acc[1][dt] = MT::mma(av, pb[1], acc[1][dt]);
+            acc[0][dt] = MT::mma(av, pl[0], acc[0][dt]);
+            acc[1][dt] = MT::mma(av, pl[1], acc[1][dt]);
+        }
+        if (copy) store_tile(tr0, dst);
+        lds_barrier();  // scores of tile t+1 and tile t+2 published; P, tile t free
     };
-    for (int it = 0; it < ntiles; it += 2) {
-        step(it, lds_t0, lds_t1);
-        if (it + 1 >= ntiles) break;
-        step(it + 1, lds_t1, lds_t0);
+    for (int t = 0;; t += 6) {
+        step(t, lds_b0, lds_b2, lds_s0);
+        if (t + 1 >= ntiles) break;
+        step(t + 1, lds_b1, lds_b0, lds_s1);
+        if (t + 2 >= ntiles) break;
+        step(t + 2, lds_b2, lds_b1, lds_s0);
+        if (t + 3 >= ntiles) break;
+        step(t + 3, lds_b0, lds_b2, lds_s1);
+        if (t + 4 >= ntiles) break;
+        step(t + 4, lds_b1, lds_b0, lds_s0);
+        if (t + 5 >= ntiles) break;
+        step(t + 5, lds_b2, lds_b1, lds_s1);
+        if (t + 6 >= ntiles) break;
     }
 
-    // l: sum over the four lane quarters that share a head
+    // l of heads 16nt + l16, from the lanes that own them
+    if (i8 == 0) lds_l[hs] = l_s;
+    lds_barrier();  // l published
+    float l[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        l[nt] += __shfl_xor(l[nt], 16);
-        l[nt] += __shfl_xor(l[nt], 32);
-    }
+    for (int nt = 0; nt < 2; ++nt) l[nt] = lds_l[16 * nt + l16];
     if (p.splits == 1) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int head = hg * kMHeads + 16 * nt + l16;
             if (head >= p.heads) continue;
-            float* out = p.u + static_cast<size_t>(head) * KL + 128 * wave + 4 * q4;
+            float* out = p.u + static_cast<size_t>(head) * KL + 128 * pw + 4 * q4;
             const float inv = 1.f / l[nt];
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
                 *reinterpret_cast<float4*>(out + 16 * dt) =
                     make_float4(acc[nt][dt][0] * inv, acc[nt][dt][1] * inv, acc[nt][dt][2] * inv, acc[nt][dt][3] * inv);
         }
+        lds_barrier();  // matches the QK waves' barriers
+        lds_barrier();
         return;
     }
     // Normalised split result u_s = acc / l, stored as fp16 u_s / 2^e with e per (head,
     // split) such that the head's largest |u_s| lands in [2^14, 2^15): no overflow and
     // full fp16 precision whatever the latent's range.  A lane holds 4 dims of each of 8
     // dim tiles of its head, so it would store 8 bytes into each of 16 head rows per
-    // instruction; the rows are assembled in LDS first (tile buffer 0, free after the
-    // barrier) and every wave store then writes one whole 1 KiB head row.
+    // instruction; the rows are assembled in LDS first (heads 0-15 in tile buffer 0,
+    // 16-31 in buffer 1, both free after the last step) and every wave store then
+    // writes one whole 1 KiB head row.
     constexpr int SR = KL * 2 + 16;  // staged row pitch (bytes)
-    static_assert(kMHeads * SR <= TB, "staged partials must fit in one tile buffer");
+    static_assert(16 * SR <= TB, "16 staged partial rows must fit in one tile buffer");
     float inv[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -530,17 +611,17 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(acc[nt][dt][r] * inv[nt]));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        if (q4 == 0) lds_amax[wave][16 * nt + l16] = amax;
+        amax = max_xor32(max_xor16(amax));
+        if (q4 == 0) lds_amax[pw][16 * nt + l16] = amax;
     }
-    lds_barrier();  // every wave is done with the last tile; lds_amax is complete
+    lds_barrier();  // amax published
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int hl = 16 * nt + l16;
         const float amax = fmaxf(fmaxf(lds_amax[0][hl], lds_amax[1][hl]), fmaxf(lds_amax[2][hl], lds_amax[3][hl]));
         // e = floor(log2(amax)) - 14 for finite non-zero amax (subnormals included)
         const int e = amax > 0.f && amax <= 3.4e38f ? ilogbf(amax) - 14 : 0;
+        char* stage = (nt ? lds_b1 : lds_b0) + l16 * SR;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -549,22 +630,27 @@ __global__ void __launch_bounds__(256) mla_tile_kernel(const MlaMK p) {
                 f32x2_t{ldexpf(acc[nt][dt][0] * inv[nt], -e), ldexpf(acc[nt][dt][1] * inv[nt], -e)}, f16x2_t);
             const f16x2_t hi = __builtin_convertvector(
                 f32x2_t{ldexpf(acc[nt][dt][2] * inv[nt], -e), ldexpf(acc[nt][dt][3] * inv[nt], -e)}, f16x2_t);
-            *reinterpret_cast<uint2*>(lds_t0 + hl * SR + 2 * (128 * wave + 16 * dt + 4 * q4)) =
+            *reinterpret_cast<uint2*>(stage + 2 * (128 * pw + 16 * dt + 4 * q4)) =
                 make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
         }
-        const int head = hg * kMHeads + hl;
-        if (wave == 0 && q4 == 0 && head < p.heads)
-            p.part_ml[static_cast<size_t>(head) * p.splits + split] =
-                make_float4(m[nt], l[nt], static_cast<float>(e), 0.f);
     }
-    lds_barrier();
-    // wave w writes head rows w, w + 4, ...: lane j the 16 bytes at 16 j
+    {
+        // (m, l, e) of head hs, from the lanes that own it
+        const float amax = fmaxf(fmaxf(lds_amax[0][hs], lds_amax[1][hs]), fmaxf(lds_amax[2][hs], lds_amax[3][hs]));
+        const int e = amax > 0.f && amax <= 3.4e38f ? ilogbf(amax) - 14 : 0;
+        const int head = hg * kMHeads + hs;
+        if (i8 == 0 && head < p.heads)
+            p.part_ml[static_cast<size_t>(head) * p.splits + split] = make_float4(m_s, l_s, static_cast<float>(e), 0.f);
+    }
+    lds_barrier();  // partial rows staged
+    // PV wave pw writes head rows pw, pw + 4, ...: lane j the 16 bytes at 16 j
 #pragma unroll
     for (int i = 0; i < kMHeads / 4; ++i) {
-        const int hl = wave + 4 * i;
+        const int hl = pw + 4 * i;
         const int head = hg * kMHeads + hl;
         if (head >= p.heads) break;
-        const U32x4 v = *reinterpret_cast<const U32x4*>(lds_t0 + hl * SR + 16 * lane);
+        const char* stage = (hl < 16 ? lds_b0 : lds_b1) + (hl & 15) * SR;
+        const U32x4 v = *reinterpret_cast<const U32x4*>(stage + 16 * lane);
         *reinterpret_cast<U32x4*>(static_cast<char*>(p.part_u) +
                                   (static_cast<size_t>(head) * p.splits + split) * (KL * 2) + 16 * lane) = v;
     }
@@ -687,7 +773,7 @@ MlaPlan plan_mla(const MlaArgs& a) {
 namespace {
 template <bool SRC_BF16, int KR>
 hipError_t launch_tile(const MlaMK& k, hipStream_t stream) {
-    hipLaunchKernelGGL((mla_tile_kernel<SRC_BF16, KR>), dim3(8 * k.per_xcd), dim3(256), 0, stream, k);
+    hipLaunchKernelGGL((mla_tile_kernel<SRC_BF16, KR>), dim3(8 * k.per_xcd), dim3(kMWaves * 64), 0, stream, k);
     return hipGetLastError();
 }
 }  // namespace
