@@ -177,8 +177,8 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
                 x[kk][i] = load_q(p.q, p.q_dtype, qrow + 32 * kk + 8 * q4 + i);
                 amax = fmaxf(amax, fabsf(x[kk][i]));
             }
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        amax = max_xor16(amax);
+        amax = max_xor32(amax);
         int qexp = 0;
         if (!BF16 && amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
         const float down = ldexpf(1.f, -qexp);
@@ -282,8 +282,8 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
                 tmax = fmaxf(tmax, fmaxf(fmaxf(sc[j][mt][0], sc[j][mt][1]), fmaxf(sc[j][mt][2], sc[j][mt][3])));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            tmax = max_xor16(tmax);
+            tmax = max_xor32(tmax);
             ts[j] = tmax * sscale[j];
             grow[j] = ts[j] > m[j] + 8.f;
             any_rescale |= grow[j] && m[j] != -INFINITY;

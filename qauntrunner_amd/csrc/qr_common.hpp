@@ -137,6 +137,28 @@ __device__ __forceinline__ float group_sum(float x, int lanes) {
     return x;
 }
 
+// Pair reductions across rows of 16 lanes (gfx950 v_permlane16_swap / v_permlane32_swap,
+// no LDS round trip): every lane gets op(x of its lane, x of lane ^ 16) (resp. ^ 32).
+// The swap hands each lane the values of both lanes of its pair (element 0 the lower
+// lane's, element 1 the upper's, checked on gfx950), so both lanes combine the same two
+// operands in the same order and end bit-identical.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------- 16-byte vector loads

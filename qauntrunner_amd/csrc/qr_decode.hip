@@ -448,8 +448,8 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
             qf[kk][i] = qb[static_cast<size_t>(hq) * D + 32 * kk + 8 * q4 + i] * qs;
             amax = fmaxf(amax, fabsf(qf[kk][i]));
         }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = max_xor16(amax);
+    amax = max_xor32(amax);
     int qexp = 0;
     if (!BF16 && amax > 16384.f && amax <= 3.0e38f) qexp = static_cast<int>(ceilf(log2f(amax / 16384.f)));
     const float down = ldexpf(1.f, -qexp);
@@ -489,8 +489,8 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
             s[i] = t0 + 8 * q4 + i < t_end ? sc[i >> 2][i & 3] * sscale : -INFINITY;
             tmax = fmaxf(tmax, s[i]);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = max_xor16(tmax);
+        tmax = max_xor32(tmax);
         // lazy rescale: m moves only when the step max exceeds it by more than 2^8,
         // so P = 2^(s - m) <= 256; the whole wave skips the rescale when no lane needs it
         const bool grow = tmax > m + 8.f;
@@ -559,8 +559,8 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     }
 
     // ---- merge the four waves through LDS (l is summed over the lane quarters first)
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = sum_xor16(l);
+    l = sum_xor32(l);
     __shared__ float sm_acc[kWaves][kMfmaGroup][D];
     __shared__ float sm_m[kWaves][kMfmaGroup];
     __shared__ float sm_l[kWaves][kMfmaGroup];

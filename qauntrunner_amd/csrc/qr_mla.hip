@@ -203,18 +203,6 @@ __device__ __forceinline__ int row_swizzle(int r) {
     return ((x & 1) << 2) | (x & 2) | (x >> 2);
 }
 
-// max(x of this lane, x of lane ^ 16) / (lane ^ 32), the same value in both lanes:
-// v_permlane16_swap / v_permlane32_swap hand each lane the values of both lanes of
-// its pair (checked on gfx950: element 0 the lower lane's, element 1 the upper's).
-__device__ __forceinline__ float max_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 // MFMA operands in the cache's own 16-bit type.
 template <bool SRC_BF16> struct PvType;
 template <> struct PvType<false> {
