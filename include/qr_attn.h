@@ -125,12 +125,34 @@ int qr_kv_append_rope(qr_kv* kv, int seq_id, int layer, int pos, float* q, const
  * each 16-byte aligned; enqueued on `stream`. */
 int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q_dev,
                           const float* k_dev, const float* v_dev, float theta, void* stream);
+/* Same for ONE position whose index is read on the device from *pos_dev (the Ensure +
+ * Append of StreamingEngine.cs:245-248 with PagedKvCache.Ensure, PagedKvCache.cs:41-60,
+ * done on the GPU): the pages up to the position are claimed from the pool by a device
+ * counter and SeqLen's device copy grows to pos + 1, so a decode step built from this
+ * call and qr_kv_attention_step_dev can be captured in a HIP graph and replayed at
+ * advancing positions.  The pool cannot grow inside a capture: reserve enough pages
+ * (qr_kv_reserve) before capturing, and make the cache's first device-side call outside
+ * capture.  A full pool or a position outside [0, max_seq) skips the append and is
+ * reported by the next host-side call on the cache (which waits for the device and
+ * reads the page accounting back; QR_ERR_OUT_OF_MEMORY / QR_ERR_OUT_OF_RANGE).  Calls
+ * on one cache must be ordered by the caller (one stream, or synchronised). */
+int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_dev, float* q_dev,
+                               const float* k_dev, const float* v_dev, float theta, void* stream);
 
 /* Attention(layer, pos, q, attn, scale), PagedKvCache.cs:83-136:
  * attn[h*D:(h+1)*D] = softmax(q_h . K[0..pos, kvh(h)] * scale) . V[0..pos, kvh(h)],
  * kvh(h) = h*kv_heads/heads.  q and attn are host fp32 [heads*head_dim]. */
 int qr_kv_attention(qr_kv* kv, int seq_id, int layer, int pos, const float* q, float* attn,
                     float scale);
+
+/* Attention (PagedKvCache.cs:83-136) for n <= 64 entries whose positions are read on
+ * the device, entry i over sequence seq_ids[i] at position pos_dev[i] (device int32
+ * array): the companion of qr_kv_append_rope_step_dev for captured decode steps.  The
+ * split plan is the one for max_seq (work past a position exits at once); the split
+ * workspace can only grow outside a capture, so make one call before capturing.
+ * Positions never appended read undefined values, as in the reference. */
+int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev,
+                             const float* q_dev, float* attn_dev, float scale, void* stream);
 
 /* n independent decode queries, entry i over sequence seq_ids[i] at position
  * pos[i]; q/attn are host fp32 [n][heads*head_dim].  Equivalent to n

@@ -70,6 +70,17 @@ def _dev_tensor(x, numel, code, what, allow_none=False):
     return ctypes.c_void_p(x.data_ptr())
 
 
+def _dev_int32(x, numel, what):
+    """Checks a device int32 tensor (positions read by the kernels) the same way."""
+    if x is None or not getattr(x, "is_cuda", False):
+        raise ValueError(f"{what}: expected an int32 tensor on the GPU")
+    if not x.is_contiguous() or str(x.dtype) != "torch.int32":
+        raise ValueError(f"{what}: expected a contiguous int32 tensor")
+    if x.numel() != numel:
+        raise ValueError(f"{what}: expected {numel} elements, got {x.numel()}")
+    return ctypes.c_void_p(x.data_ptr())
+
+
 def _rows_of(x, width, what):
     n = x.numel() // width if x is not None else 0
     if x is None or n * width != x.numel():
@@ -192,6 +203,18 @@ class PagedKvCache:
         check(self._lib.qr_kv_append_rope_dev(self._h, seq_id, layer, pos0, n, qp, kp, vp, theta,
                                               _stream_ptr(stream)))
 
+    def AppendRopeStepDev(self, layer, pos_dev, q_row, k_row, v_row, theta, seq_id=0, stream=None) -> None:
+        """AppendRopeDev of one position whose index is read on the GPU from pos_dev (int32
+        [1]); its page is claimed on the device, so the call can be captured in a graph and
+        replayed at advancing positions (pages must be reserved before capture)."""
+        f32 = _lib.DTYPE_F32
+        pp = _dev_int32(pos_dev, 1, "pos")
+        qp = _dev_tensor(q_row, self.Heads * self.HeadDim, f32, "q row", allow_none=True)
+        kp = _dev_tensor(k_row, self.KvDim, f32, "k row")
+        vp = _dev_tensor(v_row, self.KvDim, f32, "v row")
+        check(self._lib.qr_kv_append_rope_step_dev(self._h, seq_id, layer, pp, qp, kp, vp, theta,
+                                                   _stream_ptr(stream)))
+
     def Reset(self, seq_id=-1) -> None:  # PagedKvCache.cs:72
         check(self._lib.qr_kv_reset(self._h, seq_id))
 
@@ -242,6 +265,18 @@ class PagedKvCache:
         op = _dev_tensor(out, rows, _lib.DTYPE_F32, "out")
         check(self._lib.qr_kv_attention_dev_noalloc(self._h, ids.size, _ptr(ids), layer, _ptr(pos), qp, op, scale,
                                                     _stream_ptr(stream)))
+
+    def AttentionStepDev(self, layer, seq_ids, pos_dev, q, out, scale, stream=None) -> None:
+        """AttentionDev with the positions read on the GPU from pos_dev (int32, one per entry):
+        entry i attends positions 0..pos_dev[i] (graph-capturable; the split plan is the one
+        for max_seq)."""
+        ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        rows = ids.size * self.Heads * self.HeadDim
+        pp = _dev_int32(pos_dev, ids.size, "pos")
+        qp = _dev_tensor(q, rows, _lib.DTYPE_F32, "q")
+        op = _dev_tensor(out, rows, _lib.DTYPE_F32, "out")
+        check(self._lib.qr_kv_attention_step_dev(self._h, ids.size, _ptr(ids), layer, pp, qp, op, scale,
+                                                 _stream_ptr(stream)))
 
     def DecodePlan(self, layer, seq_ids, positions):
         """(tokens per split, splits of the longest entry) that a decode call with these

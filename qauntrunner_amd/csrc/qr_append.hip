@@ -123,25 +123,25 @@ __device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g,
 __host__ __device__ constexpr int v_tile_tokens(int head_dim, int tpt) { return 2 * kRopeThreads / head_dim * tpt; }
 
 template <int TPT>
-__device__ __forceinline__ void v_tile_store(const AppendArgs& g, int vb) {
+__device__ __forceinline__ void v_tile_store(const AppendArgs& g, int pos0, int vb) {
     static_assert(TPT % 8 == 0, "whole 16-byte chunks");
     const int D = g.geom.head_dim;
     const int pairs = D >> 1;  // 32 or 64
     const int T = v_tile_tokens(D, TPT);
     const int kvh = vb % g.geom.kv_heads;
-    const int tbase = (g.pos0 / T + vb / g.geom.kv_heads) * T;
+    const int tbase = (pos0 / T + vb / g.geom.kv_heads) * T;
     const int dp = threadIdx.x & (pairs - 1);
     const int t0 = tbase + (threadIdx.x / pairs) * TPT;
     const float* src = static_cast<const float*>(g.src[1]) + kvh * D + 2 * dp;
     float2 v[TPT];
 #pragma unroll
     for (int k = 0; k < TPT; ++k) {
-        const int r = min(max(t0 + k - g.pos0, 0), g.n - 1);
+        const int r = min(max(t0 + k - pos0, 0), g.n - 1);
         v[k] = *reinterpret_cast<const float2*>(src + static_cast<long long>(r) * g.src_stride);
     }
     const long long phys = g.page_table[tbase >> kPageShift];
     const int slot0 = t0 & (kPageTokens - 1);
-    const bool whole = t0 >= g.pos0 && t0 + TPT <= g.pos0 + g.n;
+    const bool whole = t0 >= pos0 && t0 + TPT <= pos0 + g.n;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         uint16_t b[TPT];
@@ -162,7 +162,7 @@ __device__ __forceinline__ void v_tile_store(const AppendArgs& g, int vb) {
         } else {
 #pragma unroll
             for (int k = 0; k < TPT; ++k)
-                if (t0 + k >= g.pos0 && t0 + k < g.pos0 + g.n) p[k] = b[k];
+                if (t0 + k >= pos0 && t0 + k < pos0 + g.n) p[k] = b[k];
         }
     }
 }
@@ -174,8 +174,13 @@ __device__ __forceinline__ void v_tile_store(const AppendArgs& g, int vb) {
 template <int IPT, int TPT>
 __global__ void __launch_bounds__(kRopeThreads) rope_append_items_kernel(const RopeAppendArgs a, int nv) {
     const AppendArgs& g = a.app;
+    int pos0 = g.pos0;
+    if (g.pos_dev) {  // device-side position: written only where its page was claimed
+        pos0 = *g.pos_dev;
+        if (pos0 < 0 || pos0 >= g.max_seq || (pos0 >> kPageShift) >= *g.held_dev) return;
+    }
     if (TPT > 0 && static_cast<int>(blockIdx.x) < nv) {
-        v_tile_store<TPT ? TPT : 8>(g, blockIdx.x);
+        v_tile_store<TPT ? TPT : 8>(g, pos0, blockIdx.x);
         return;
     }
     const int D = g.geom.head_dim;
@@ -204,12 +209,12 @@ __global__ void __launch_bounds__(kRopeThreads) rope_append_items_kernel(const R
     }
     __shared__ float cs[2][kMaxRopeHalf];
     for (int i = threadIdx.x; i < half; i += kRopeThreads) {
-        const float ang = mul_rn(static_cast<float>(g.pos0 + row), a.freq[i]);
+        const float ang = mul_rn(static_cast<float>(pos0 + row), a.freq[i]);
         cs[0][i] = cosf(ang);
         cs[1][i] = sinf(ang);
     }
     __syncthreads();
-    const int t = g.pos0 + static_cast<int>(row);
+    const int t = pos0 + static_cast<int>(row);
     const long long phys = g.page_table[t >> kPageShift];
     const int slot = t & (kPageTokens - 1);
 #pragma unroll
@@ -323,6 +328,35 @@ hipError_t launch_append(const AppendArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// One thread: the pages a device-side position needs, from the pool's device counter.
+__global__ void __launch_bounds__(64) page_claim_kernel(const PageClaimArgs a) {
+    if (threadIdx.x != 0) return;
+    const int pos = *a.pos_dev;
+    if (pos < 0 || pos >= a.max_seq) {
+        atomicOr(&a.state[1], 2);
+        return;
+    }
+    const int need = (pos >> kPageShift) + 1;
+    const int held = a.state[a.held_index];
+    if (need > held) {
+        const int cnt = need - held;
+        const int first = atomicAdd(&a.state[0], cnt);
+        if (first + cnt > a.capacity) {
+            atomicSub(&a.state[0], cnt);
+            atomicOr(&a.state[1], 1);
+            return;
+        }
+        for (int i = 0; i < cnt; ++i) a.page_table[held + i] = first + i;
+        a.state[a.held_index] = need;
+    }
+    atomicMax(&a.state[a.seq_index], pos + 1);  // PagedKvCache.cs:68
+}
+
+hipError_t launch_page_claim(const PageClaimArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(page_claim_kernel, dim3(1), dim3(64), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
     const long long total = static_cast<long long>(a.n) * a.geom.kv_heads * a.geom.head_dim * a.geom.planes;
     if (total == 0) return hipSuccess;
@@ -332,6 +366,7 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
+    if (a.app.pos_dev && a.app.n != 1) return hipErrorInvalidValue;  // one device-side position
     const int D = a.app.geom.head_dim;
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
     const int ipt = (heads * (D / 8) + kRopeThreads - 1) / kRopeThreads;
@@ -358,6 +393,7 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     case 6: QR_ROPE_ITEMS(6); break;
     case 7: case 8: QR_ROPE_ITEMS(8); break;
     default:
+        if (a.app.pos_dev) return hipErrorInvalidValue;  // device positions: the item kernel only
         hipLaunchKernelGGL(rope_append_kernel, dim3((a.app.n + kRopeRows - 1) / kRopeRows), dim3(256), 0, stream, a);
     }
 #undef QR_ROPE_ITEMS

@@ -74,7 +74,13 @@ struct DecodeK {
     int split_tokens;
     int seq_len[kMaxDecodeBatch];
     int pt_off[kMaxDecodeBatch];
+    const int* pos_dev;  // device positions (seq = pos + 1, clamped to [1, seq_len]) when set
 };
+
+// Positions attended by entry b: seq_len[b], or a device position + 1 bounded by it.
+__device__ __forceinline__ int entry_seq(const DecodeK& p, int b) {
+    return p.pos_dev ? min(max(p.pos_dev[b] + 1, 1), p.seq_len[b]) : p.seq_len[b];
+}
 
 __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
@@ -92,7 +98,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     const int split = blockIdx.x;
     const int unit = blockIdx.y;
     const int b = blockIdx.z;
-    const int seq = p.seq_len[b];
+    const int seq = entry_seq(p, b);
     const int t_begin = split * p.split_tokens;
     if (t_begin >= seq) return;
     const int t_end = min(seq, t_begin + p.split_tokens);
@@ -384,7 +390,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     const int split = blockIdx.x;
     const int unit = blockIdx.y;
     const int b = blockIdx.z;
-    const int seq = p.seq_len[b];
+    const int seq = entry_seq(p, b);
     const int t_begin = split * p.split_tokens;
     if (t_begin >= seq) return;
     const int t_end = min(seq, t_begin + p.split_tokens);
@@ -606,7 +612,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
 __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK p) {
     const int h = blockIdx.x;
     const int b = blockIdx.y;
-    const int seq = p.seq_len[b];
+    const int seq = entry_seq(p, b);
     const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
     if (nsplit <= 1) return;
     const int D = p.head_dim;
@@ -869,6 +875,7 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
         k.seq_len[i] = a.seq_len[i];
         k.pt_off[i] = a.pt_off[i];
     }
+    k.pos_dev = a.pos_dev;
     if (pl.max_splits > kMaxSplits) return hipErrorInvalidValue;
     const void* fn;
     if (uses_mfma(a)) {

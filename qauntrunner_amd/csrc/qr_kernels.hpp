@@ -47,8 +47,30 @@ struct AppendArgs {
     int src_dtype;
     int pos0;
     int n;
+    // Device-side position (single-position appends): when set, pos0 is *pos_dev, read
+    // by the kernel, and the row is written only if the page of that position is held
+    // (*held_dev pages) and the position lies in [0, max_seq).
+    const int* pos_dev;
+    const int* held_dev;
+    int max_seq;
 };
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
+
+// Device-side page claim for one appended position read from *pos_dev: pages
+// held..(pos >> 8) of one (sequence, layer) get the next indices of the pool's
+// device counter and their page-table entries; SeqLen's device copy grows to pos + 1.
+// state: [0] pages handed out, [1] error bits (1: pool full, 2: position outside
+// [0, max_seq)), then `held` and `seq_len` entries at the given indices.
+struct PageClaimArgs {
+    int* page_table;   // entries of this (sequence, layer)
+    int* state;
+    int held_index;    // index of this (sequence, layer)'s held count in state
+    int seq_index;     // index of the sequence's SeqLen in state
+    int capacity;      // pages in the pool
+    int max_seq;
+    const int* pos_dev;
+};
+hipError_t launch_page_claim(const PageClaimArgs& a, hipStream_t stream);
 
 // Gathers rows back out in the cache dtype ([n][kv_heads*head_dim] per plane),
 // or decoded to fp32 when to_f32 is set.
@@ -96,6 +118,9 @@ struct DecodeArgs {
     int nb;
     int seq_len[kMaxDecodeBatch];  // positions attended per entry (pos + 1)
     int pt_off[kMaxDecodeBatch];   // offset of the entry's page-table row
+    // Device-side positions: when set, entry b attends positions 0..pos_dev[b] (read by
+    // the kernels, clamped to [0, seq_len[b] - 1]); seq_len[b] then only bounds the plan.
+    const int* pos_dev;
 };
 
 // Split-K plan for one launch.

@@ -25,6 +25,7 @@ struct qr_kv {
     DevBuf workspace;  // split-K partials
     hipEvent_t split_event = nullptr;  // benchmark instrumentation (qr_kv_set_split_event)
     void* scratch = nullptr;           // this device's decode scratch array (no-allocation calls)
+    bool device_steps = false;         // the device copy of the page accounting is in use
 };
 
 namespace {
@@ -62,6 +63,26 @@ int check_resident(const qr_kv* kv, int seq_id, int layer, int pos) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// Host view of the page accounting and SeqLen, read back from the device after
+// device-side appends (a no-op otherwise).
+int sync_host(const qr_kv* ckv) {
+    qr_kv* kv = const_cast<qr_kv*>(ckv);
+    if (!kv->store.device_ahead()) return QR_OK;
+    DeviceGuard dg(kv->device);
+    return kv->store.pull(kv->seq_len);
+}
+
+// Device copy of the accounting after host-side changes (once device-side appends are in use).
+int sync_device(qr_kv* kv, hipStream_t stream) {
+    if (!kv->device_steps) return QR_OK;
+    return kv->store.push(kv->seq_len, stream);
+}
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 // Appends rows already on the device (src_dtype, row stride kv_dim).
 int append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k, const void* v,
                int k_len, int v_len, int src_dtype, hipStream_t stream) {
@@ -82,7 +103,7 @@ int append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, const void* k,
     QR_HIP(launch_append(a, stream));
     int& sl = kv->seq_len[seq_id];
     sl = std::max(sl, pos0 + n);  // PagedKvCache.cs:68
-    return QR_OK;
+    return sync_device(kv, stream);
 }
 
 // RoPE + append of n positions from device rows (fp32 k/v, q rotated in place).
@@ -111,7 +132,7 @@ int rope_append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q,
     QR_HIP(launch_rope_append(a, stream));
     int& sl = kv->seq_len[seq_id];
     sl = std::max(sl, pos0 + n);  // PagedKvCache.cs:68
-    return QR_OK;
+    return sync_device(kv, stream);
 }
 
 // Runs decode entries (seq_ids[i], seq_len[i]) with device q/out rows.
@@ -242,6 +263,7 @@ int qr_kv_destroy(qr_kv* kv) {
 int qr_kv_reserve(qr_kv* kv, int pages) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     DeviceGuard dg(kv->device);
     return kv->store.reserve(pages);
 }
@@ -250,6 +272,7 @@ int qr_kv_append(qr_kv* kv, int seq_id, int layer, int pos, const float* k, int 
                  int v_len) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_TRY(check_pos(kv, pos));
     QR_CHECK_ARG(k_len >= 0 && v_len >= 0, "negative row length");
@@ -273,6 +296,7 @@ int qr_kv_append_range(qr_kv* kv, int seq_id, int layer, int pos0, int n, const 
                        int src_dtype) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
@@ -295,6 +319,7 @@ int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, co
                            const void* v_dev, int src_dtype, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
@@ -311,6 +336,7 @@ int qr_kv_append_rope(qr_kv* kv, int seq_id, int layer, int pos, float* q, const
                       float theta) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_TRY(check_pos(kv, pos));
     QR_CHECK_ARG(q && k && v, "null q/k/v row");
@@ -335,6 +361,7 @@ int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, flo
                           const float* v_dev, float theta, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
     QR_CHECK_ARG(n == 0 || (k_dev && v_dev), "null k/v rows");
@@ -355,6 +382,7 @@ int qr_kv_attention_batch(qr_kv* kv, int n, const int* seq_ids, int layer, const
                           float* attn, float scale) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(q && attn, "null q/attn pointer");
     std::vector<int> seq_len;
     QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
@@ -374,6 +402,7 @@ int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const i
                         float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
     std::vector<int> seq_len;
     QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
@@ -385,6 +414,7 @@ int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer,
                                 const float* q_dev, float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
     QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for the no-allocation call", n,
                  kMaxDecodeBatch);
@@ -485,6 +515,7 @@ int qr_kv_attention_chunk(qr_kv* kv, int seq_id, int layer, int pos0, int nq, co
                           float* attn, float scale) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     return chunk_common(kv, seq_id, layer, pos0, nq, q, q_dtype, attn, false, false, scale, kv->stream);
 }
 
@@ -492,6 +523,7 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
                               int q_dtype, float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     return chunk_common(kv, seq_id, layer, pos0, nq, q_dev, q_dtype, attn_dev, true, true, scale,
                         as_stream(stream));
 }
@@ -500,6 +532,7 @@ int qr_kv_decode_plan(qr_kv* kv, int n, const int* seq_ids, int layer, const int
                       int* splits) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(split_tokens && splits, "null output pointer");
     std::vector<int> seq_len;
     QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
@@ -526,26 +559,39 @@ int qr_kv_set_split_event(qr_kv* kv, void* event) {
 int qr_kv_reset(qr_kv* kv, int seq_id) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     if (seq_id < 0) {
         std::fill(kv->seq_len.begin(), kv->seq_len.end(), 0);
-        return QR_OK;
+    } else {
+        QR_CHECK_ARG(seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
+        kv->seq_len[seq_id] = 0;
     }
-    QR_CHECK_ARG(seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
-    kv->seq_len[seq_id] = 0;
+    if (kv->device_steps) {
+        DeviceGuard dg(kv->device);
+        QR_TRY(sync_device(kv, kv->stream));
+        QR_HIP(hipStreamSynchronize(kv->stream));
+    }
     return QR_OK;
 }
 
 int qr_kv_truncate(qr_kv* kv, int seq_id, int len) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(seq_id >= 0 && seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
     if (len < kv->seq_len[seq_id]) kv->seq_len[seq_id] = len;  // PagedKvCache.cs:76
+    if (kv->device_steps) {
+        DeviceGuard dg(kv->device);
+        QR_TRY(sync_device(kv, kv->stream));
+        QR_HIP(hipStreamSynchronize(kv->stream));
+    }
     return QR_OK;
 }
 
 int qr_kv_seq_len(const qr_kv* kv, int seq_id, int* out) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(out, "null output pointer");
     QR_CHECK_ARG(seq_id >= 0 && seq_id < kv->max_batch, "seq_id %d outside [0, %d)", seq_id, kv->max_batch);
     *out = kv->seq_len[seq_id];
@@ -555,6 +601,7 @@ int qr_kv_seq_len(const qr_kv* kv, int seq_id, int* out) {
 int qr_kv_bytes_used(const qr_kv* kv, long long* out) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_CHECK_ARG(out, "null output pointer");
     *out = kv->store.bytes_used();
     return QR_OK;
@@ -571,6 +618,7 @@ int qr_kv_bytes_per_token(const qr_kv* kv, long long* out) {
 int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, void* v_out) {
     clear_error();
     QR_TRY(check_handle(kv));
+    QR_TRY(sync_host(kv));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
     QR_CHECK_ARG(n == 0 || (k_out && v_out), "null output rows");
@@ -599,4 +647,96 @@ int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, v
     return QR_OK;
 }
 
+int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_dev, float* q_dev,
+                               const float* k_dev, const float* v_dev, float theta, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(pos_dev && k_dev && v_dev, "null pos/k/v pointer");
+    DeviceGuard dg(kv->device);
+    const hipStream_t st = as_stream(stream);
+    const bool cap = capturing(st);
+    if (!kv->device_steps) {
+        // first device-side append: the device copy starts from the host accounting
+        QR_CHECK_ARG(!cap, "the first device-side append of a cache must run outside stream capture");
+        QR_TRY(sync_host(kv));
+        kv->device_steps = true;
+        QR_TRY(kv->store.push(kv->seq_len, st));
+    }
+    if (kv->store.capacity() < 1) {
+        QR_CHECK_ARG(!cap, "the page pool is empty: reserve pages before capturing device-side appends");
+        QR_TRY(kv->store.reserve(16));
+    }
+    PageClaimArgs c{};
+    c.page_table = const_cast<int*>(kv->store.page_table_dev()) + kv->store.pt_offset(seq_id, layer);
+    c.state = kv->store.state_dev();
+    c.held_index = kv->store.held_index(seq_id, layer);
+    c.seq_index = kv->store.seq_index(seq_id);
+    c.capacity = static_cast<int>(std::min<long long>(kv->store.capacity(), 0x7FFFFFFF));
+    c.max_seq = kv->max_seq;
+    c.pos_dev = pos_dev;
+    QR_HIP(launch_page_claim(c, st));
+    RopeAppendArgs a{};
+    a.app.pool = kv->store.pool();
+    a.app.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+    a.app.geom = kv->store.geom();
+    a.app.dtype = kv->dtype;
+    a.app.src[0] = k_dev;
+    a.app.src[1] = v_dev;
+    a.app.row_len[0] = kv->kv_dim;
+    a.app.row_len[1] = kv->kv_dim;
+    a.app.src_stride = kv->kv_dim;
+    a.app.src_dtype = QR_DTYPE_F32;
+    a.app.pos0 = 0;
+    a.app.n = 1;
+    a.app.pos_dev = pos_dev;
+    a.app.held_dev = kv->store.state_dev() + c.held_index;
+    a.app.max_seq = kv->max_seq;
+    a.q = q_dev;
+    a.q_width = kv->heads * kv->head_dim;
+    const int half = kv->head_dim / 2;
+    for (int i = 0; i < half; ++i) a.freq[i] = std::pow(theta, (-2.0f * static_cast<float>(i)) / static_cast<float>(kv->head_dim));
+    QR_HIP(launch_rope_append(a, st));
+    kv->store.mark_device_ahead();
+    return QR_OK;
+}
+
+int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev,
+                             const float* q_dev, float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(q_dev && attn_dev && pos_dev, "null q/attn/pos pointer");
+    QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for device positions", n,
+                 kMaxDecodeBatch);
+    QR_CHECK_ARG(seq_ids, "null seq_ids array");
+    DeviceGuard dg(kv->device);
+    const hipStream_t st = as_stream(stream);
+    QR_CHECK_ARG(kv->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
+    DecodeArgs a{};
+    for (int i = 0; i < n; ++i) {
+        QR_TRY(check_seq_layer(kv, seq_ids[i], layer));
+        a.seq_len[i] = kv->max_seq;  // bound of the plan; the kernels read the positions
+        a.pt_off[i] = kv->store.pt_offset(seq_ids[i], layer);
+    }
+    a.pool = kv->store.pool();
+    a.page_table = kv->store.page_table_dev();
+    a.geom = kv->store.geom();
+    a.dtype = kv->dtype;
+    a.heads = kv->heads;
+    a.q = q_dev;
+    a.out = attn_dev;
+    a.scale = scale;
+    a.nb = n;
+    a.pos_dev = pos_dev;
+    const DecodePlan plan = plan_decode(a);
+    const size_t ws = std::max<size_t>(plan.workspace_bytes, 256);
+    if (ws > kv->workspace.size()) {
+        QR_CHECK_ARG(!capturing(st), "the split workspace must grow to %zu bytes: make one call outside capture first", ws);
+        QR_TRY(kv->workspace.ensure(ws));
+    }
+    QR_HIP(launch_decode(a, plan, kv->workspace.get(), st, nullptr));
+    return QR_OK;
+}
+
 }  // extern "C"
+

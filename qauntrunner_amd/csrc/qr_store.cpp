@@ -47,6 +47,7 @@ int DevBuf::ensure(size_t bytes, bool zero) {
 PagedStore::~PagedStore() {
     if (pool_) (void)hipFree(pool_);
     if (pt_dev_) (void)hipFree(pt_dev_);
+    if (state_dev_) (void)hipFree(state_dev_);
 }
 
 int PagedStore::init(const PageGeom& geom, int dtype, int layers, int seqs, int max_seq) {
@@ -60,6 +61,36 @@ int PagedStore::init(const PageGeom& geom, int dtype, int layers, int seqs, int 
     held_.assign(static_cast<size_t>(seqs) * layers, 0);
     QR_HIP(hipMalloc(&pt_dev_, std::max<size_t>(entries, 1) * sizeof(int)));
     QR_HIP(hipMemset(pt_dev_, 0, std::max<size_t>(entries, 1) * sizeof(int)));
+    state_host_.assign(2 + static_cast<size_t>(seqs) * layers + seqs, 0);
+    QR_HIP(hipMalloc(&state_dev_, state_host_.size() * sizeof(int)));
+    QR_HIP(hipMemset(state_dev_, 0, state_host_.size() * sizeof(int)));
+    return QR_OK;
+}
+
+int PagedStore::pull(std::vector<int>& seq_len) {
+    if (!device_ahead_) return QR_OK;
+    QR_HIP(hipDeviceSynchronize());  // the device-side appends were enqueued on caller streams
+    QR_HIP(hipMemcpy(state_host_.data(), state_dev_, state_host_.size() * sizeof(int), hipMemcpyDeviceToHost));
+    device_ahead_ = false;
+    pages_used_ = state_host_[0];
+    for (size_t i = 0; i < held_.size(); ++i) held_[i] = state_host_[2 + i];
+    for (int s = 0; s < seqs_; ++s) seq_len[s] = state_host_[seq_index(s)];
+    const int err = state_host_[1];
+    if (err) {
+        QR_HIP(hipMemset(state_dev_ + 1, 0, sizeof(int)));
+        set_error("a device-side append failed: %s%s", (err & 1) ? "the page pool was full (reserve more pages) " : "",
+                  (err & 2) ? "a position was outside [0, max_seq)" : "");
+        return (err & 1) ? QR_ERR_OUT_OF_MEMORY : QR_ERR_OUT_OF_RANGE;
+    }
+    return QR_OK;
+}
+
+int PagedStore::push(const std::vector<int>& seq_len, hipStream_t stream) {
+    state_host_[0] = static_cast<int>(pages_used_);
+    state_host_[1] = 0;
+    for (size_t i = 0; i < held_.size(); ++i) state_host_[2 + i] = held_[i];
+    for (int s = 0; s < seqs_; ++s) state_host_[seq_index(s)] = seq_len[s];
+    QR_HIP(hipMemcpyAsync(state_dev_, state_host_.data(), state_host_.size() * sizeof(int), hipMemcpyHostToDevice, stream));
     return QR_OK;
 }
 

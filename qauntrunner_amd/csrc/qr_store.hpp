@@ -65,6 +65,23 @@ public:
     long long page_bytes() const { return geom_.page_elems() * dtype_size(dtype_); }
     long long bytes_used() const { return pages_used_ * page_bytes(); }
     int max_pages() const { return max_pages_; }
+    long long capacity() const { return pool_cap_; }
+
+    // Device copy of the page accounting, for appends whose position is read on the
+    // device (page_claim_kernel): [0] pages handed out, [1] error bits, then the held
+    // count of every (seq, layer), then SeqLen of every sequence.  The host copy is
+    // authoritative until a device-side append is enqueued (mark_device_ahead); the
+    // next host-side call then waits for the device and reads it back (pull).
+    int* state_dev() const { return state_dev_; }
+    int held_index(int seq, int layer) const { return 2 + seq * layers_ + layer; }
+    int seq_index(int seq) const { return 2 + seqs_ * layers_ + seq; }
+    void mark_device_ahead() { device_ahead_ = true; }
+    bool device_ahead() const { return device_ahead_; }
+    // Waits for the device, takes pages used and held counts from its copy and stores
+    // SeqLen into seq_len; device error bits become an error return (and are cleared).
+    int pull(std::vector<int>& seq_len);
+    // Writes the host accounting and seq_len to the device copy (on `stream`).
+    int push(const std::vector<int>& seq_len, hipStream_t stream);
 
 private:
     int grow(long long min_pages);
@@ -79,6 +96,9 @@ private:
     std::vector<int> pt_host_;
     int* pt_dev_ = nullptr;
     std::vector<int> held_;
+    int* state_dev_ = nullptr;
+    std::vector<int> state_host_;
+    bool device_ahead_ = false;
 };
 
 }  // namespace qr

@@ -74,6 +74,8 @@ def test_null_handles_are_rejected():
     assert L.qr_kv_attention(None, 0, 0, 0, None, None, 1.0) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_mla_attention(None, 0, 0, 1, None, None, 1.0, None) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_mla_set_rope(None, 64) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_append_rope_step_dev(None, 0, 0, None, None, None, None, 1e4, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_attention_step_dev(None, 1, None, 0, None, None, None, 1.0, None) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_destroy(None) == 0 and L.qr_mla_destroy(None) == 0
     assert "null" in L.qr_last_error().decode() or L.qr_last_error() == b""
 
@@ -143,3 +145,13 @@ def test_device_tensor_arguments_are_checked_on_the_host():
                     (None, _lib.DTYPE_F32)):
         with pytest.raises(ValueError):
             _dev_tensor(t, 8, code, "x")
+
+
+def test_device_position_tensors_are_checked_on_the_host():
+    from qauntrunner_amd.caches import _dev_int32
+
+    assert _dev_int32(_FakeTensor(1, "torch.int32"), 1, "pos").value == 0x1000
+    for t in (_FakeTensor(2, "torch.int32"), _FakeTensor(1, "torch.int64"), _FakeTensor(1, "torch.int32", cuda=False),
+              _FakeTensor(1, "torch.int32", contiguous=False), None):
+        with pytest.raises(ValueError):
+            _dev_int32(t, 1, "pos")

@@ -1,0 +1,178 @@
+"""GPU tests of the device-position decode step: qr_kv_append_rope_step_dev (Ensure + RoPE +
+Append of StreamingEngine.cs:245-248 with PagedKvCache.Ensure, PagedKvCache.cs:41-60, on the
+device) and qr_kv_attention_step_dev (PagedKvCache.Attention, :83-136, with the position read on
+the device).
+
+Both are checked against the host-position path on a second cache fed the same rows:
+* stored K/V rows and the rotated q are bit-identical (the same kernels at the same positions);
+* attention agrees within 2e-6 of max|out| (fp32 caches) or 1e-5 (fp16 caches): the device
+  path plans its splits for max_seq, the host path for the actual length, so the split merge
+  sums in another order;
+* SeqLen, BytesUsed and the page accounting agree once the host reads the device state back,
+  and host-path appends after device steps continue on fresh pages.
+The graph test captures one step (append + attention, two layers) in a HIP graph, replays it at
+advancing positions across page boundaries with eager updates of the position and the rows in
+between, and checks every replay against the host path.
+"""
+import numpy as np
+import pytest
+
+import qauntrunner_amd as qr
+from qauntrunner_amd._lib import QrOutOfMemory, QrOutOfRange
+from tests.util import normal
+
+pytestmark = pytest.mark.gpu
+
+THETA = 500000.0
+
+
+def _rows(seed, n, heads, kv_heads, D):
+    return (normal(seed, (n, heads * D)), normal(seed + 1, (n, kv_heads * D)), normal(seed + 2, (n, kv_heads * D)))
+
+
+def _host_step(torch, kv, layer, pos, q, k, v, out):
+    """Host-position reference step: rotates q in place, appends k/v, attends 0..pos."""
+    kv.AppendRopeDev(layer, pos, q, k, v, THETA)
+    kv.AttentionDev(layer, [0], [pos], q, out, 1.0 / np.sqrt(kv.HeadDim))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_device_steps_match_the_host_path(gpu, dtype):
+    import torch
+
+    heads, kv_heads, D, max_seq = 8, 2, 128, 2048
+    p0, steps = 250, 20  # crosses the page boundary at 256
+    Q, K, V = _rows(700, p0 + steps, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, max_seq, kv_dtype=dtype) as A, \
+            qr.PagedKvCache(1, heads, kv_heads, D, max_seq, kv_dtype=dtype) as B:
+        # a prefix through the host path on both caches
+        for kv in (A, B):
+            kv.AppendRopeDev(0, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        pos_dev = torch.zeros(1, dtype=torch.int32, device=gpu)
+        for t in range(p0, p0 + steps):
+            qa, qb = dev(Q[t]), dev(Q[t])
+            oa = torch.empty(heads * D, device=gpu)
+            ob = torch.empty(heads * D, device=gpu)
+            _host_step(torch, A, 0, t, qa, dev(K[t]), dev(V[t]), oa)
+            pos_dev.fill_(t)
+            B.AppendRopeStepDev(0, pos_dev, qb, dev(K[t]), dev(V[t]), THETA)
+            B.AttentionStepDev(0, [0], pos_dev, qb, ob, scale)
+            torch.cuda.synchronize()
+            assert torch.equal(qa, qb), f"rotated q differs at {t}"
+            want, got = oa.cpu().numpy(), ob.cpu().numpy()
+            tol = (2e-6 if dtype == "f32" else 1e-5) * float(np.max(np.abs(want)))
+            assert float(np.max(np.abs(got - want))) <= tol, f"attention at {t}"
+        # the host reads the device accounting back
+        assert B.SeqLen == A.SeqLen == p0 + steps
+        assert B.BytesUsed == A.BytesUsed
+        ka, va = A.Read(0, 0, p0 + steps)
+        kb, vb = B.Read(0, 0, p0 + steps)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        # host-path appends continue after device steps
+        t = p0 + steps
+        for kv in (A, B):
+            kv.AppendRopeDev(0, t, dev(Q[t - 1]), dev(K[t - 1]), dev(V[t - 1]), THETA)
+        assert B.SeqLen == A.SeqLen == t + 1 and B.BytesUsed == A.BytesUsed
+        ka, va = A.Read(0, t, 1)
+        kb, vb = B.Read(0, t, 1)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        # Reset / Truncate reach the device copy: the next device step sees SeqLen from there
+        B.Truncate(100)
+        assert B.SeqLen == 100
+        pos_dev.fill_(100)
+        B.AppendRopeStepDev(0, pos_dev, dev(Q[0]), dev(K[0]), dev(V[0]), THETA)
+        assert B.SeqLen == 101
+
+
+def test_device_step_reports_a_full_pool_and_a_bad_position(gpu):
+    import torch
+
+    heads, kv_heads, D = 4, 2, 64
+    with qr.PagedKvCache(1, heads, kv_heads, D, 100000) as kv:
+        kv.Reserve(16)  # 16 pages: positions up to 4095
+        pos = torch.tensor([4000], dtype=torch.int32, device=gpu)
+        k = torch.ones(kv_heads * D, device=gpu)
+        kv.AppendRopeStepDev(0, pos, None, k, k, THETA)
+        assert kv.SeqLen == 4001
+        pos.fill_(5000)  # needs page 19: the pool holds 16
+        kv.AppendRopeStepDev(0, pos, None, k, k, THETA)
+        with pytest.raises(QrOutOfMemory):
+            kv.SeqLen
+        assert kv.SeqLen == 4001  # reported once; the append was skipped
+        pos.fill_(100000)  # outside [0, max_seq)
+        kv.AppendRopeStepDev(0, pos, None, k, k, THETA)
+        with pytest.raises(QrOutOfRange):
+            kv.SeqLen
+        assert kv.SeqLen == 4001
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_captured_decode_step_replays_at_advancing_positions(gpu, dtype):
+    import torch
+
+    heads, kv_heads, D, max_seq, layers = 8, 2, 128, 4096, 2
+    p0, steps = 500, 24  # crosses the page boundary at 512
+    Q, K, V = _rows(800, p0 + steps + 1, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(layers, heads, kv_heads, D, max_seq, kv_dtype=dtype) as A, \
+            qr.PagedKvCache(layers, heads, kv_heads, D, max_seq, kv_dtype=dtype) as B:
+        for kv in (A, B):
+            for layer in range(layers):
+                kv.AppendRopeDev(layer, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        B.Reserve(64)  # the pool cannot grow inside a capture
+        pos_dev = torch.zeros(1, dtype=torch.int32, device=gpu)
+        qbuf = [torch.empty(heads * D, device=gpu) for _ in range(layers)]
+        kbuf, vbuf = torch.empty(kv_heads * D, device=gpu), torch.empty(kv_heads * D, device=gpu)
+        obuf = [torch.empty(heads * D, device=gpu) for _ in range(layers)]
+
+        def step_b(stream=None):
+            for layer in range(layers):
+                B.AppendRopeStepDev(layer, pos_dev, qbuf[layer], kbuf, vbuf, THETA, stream=stream)
+                B.AttentionStepDev(layer, [0], pos_dev, qbuf[layer], obuf[layer], scale, stream=stream)
+
+        def load(t):
+            pos_dev.fill_(t)
+            kbuf.copy_(dev(K[t]))
+            vbuf.copy_(dev(V[t]))
+            for layer in range(layers):
+                qbuf[layer].copy_(dev(Q[t]))
+
+        def check(t):
+            for layer in range(layers):
+                qa, oa = dev(Q[t]), torch.empty(heads * D, device=gpu)
+                _host_step(torch, A, layer, t, qa, dev(K[t]), dev(V[t]), oa)
+                torch.cuda.synchronize()
+                assert torch.equal(qa, qbuf[layer]), f"rotated q, layer {layer}, position {t}"
+                want, got = oa.cpu().numpy(), obuf[layer].cpu().numpy()
+                tol = (2e-6 if dtype == "f32" else 1e-5) * float(np.max(np.abs(want)))
+                assert float(np.max(np.abs(got - want))) <= tol, f"attention, layer {layer}, position {t}"
+
+        # the cache's first device-side step runs eagerly (it also sizes the split workspace)
+        load(p0)
+        step_b()
+        torch.cuda.synchronize()
+        check(p0)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            load(p0 + 1)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step_b()
+        # capture does not run the work: replay every position, eager updates in between
+        for t in range(p0 + 1, p0 + steps + 1):
+            load(t)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            check(t)
+        assert B.SeqLen == A.SeqLen == p0 + steps + 1
+        assert B.BytesUsed == A.BytesUsed
+        for layer in range(layers):
+            ka, va = A.Read(layer, 0, p0 + steps + 1)
+            kb, vb = B.Read(layer, 0, p0 + steps + 1)
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}"
