@@ -78,8 +78,12 @@ struct DecodeK {
 };
 
 // Positions attended by entry b: seq_len[b], or a device position + 1 bounded by it.
+// Workgroup-uniform: the position is a scalar load (no kernel here writes positions).
 __device__ __forceinline__ int entry_seq(const DecodeK& p, int b) {
-    return p.pos_dev ? min(max(p.pos_dev[b] + 1, 1), p.seq_len[b]) : p.seq_len[b];
+    if (!p.pos_dev) return p.seq_len[b];
+    const int pos = reinterpret_cast<const __attribute__((address_space(4))) int*>(
+        reinterpret_cast<uintptr_t>(p.pos_dev))[b];
+    return __builtin_amdgcn_readfirstlane(min(max(pos + 1, 1), p.seq_len[b]));
 }
 
 __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
@@ -99,8 +103,9 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     const int unit = blockIdx.y;
     const int b = blockIdx.z;
     const int seq = entry_seq(p, b);
+    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    if (split >= nsplit) return;
     const int t_begin = split * p.split_tokens;
-    if (t_begin >= seq) return;
     const int t_end = min(seq, t_begin + p.split_tokens);
 
     const int D = DT ? DT : p.head_dim;
@@ -129,7 +134,8 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     float q[GMAX][DPL];  // filled once the first K/V step is in flight
     const int* pt = p.page_table + p.pt_off[b];
     const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
-    const int row_in_step = tg;  // + u * ntg
+    // row u of a lane's token group in a step: row_in_step + u * ntg
+    const int row_in_step = tg;
     const int nsteps = (t_end - t_begin + step_tokens - 1) / step_tokens;
 
     // Addresses are a wave-uniform 64-bit base (the step's first row in the (page, kv
@@ -155,9 +161,13 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     // cost 5% at batch 16).
     const int rot = (split * 7) % nsteps;
     auto step_t0 = [&](int st) { return t_begin + (st + rot < nsteps ? st + rot : st + rot - nsteps) * step_tokens; };
-    auto issue = [&](int st, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
-        const int t0 = step_t0(st);  // uniform: a step never crosses a page
-        const long long phys = pt[t0 >> kPageShift];
+    // t0: first row of the step (wave-uniform: a step never crosses a page)
+    auto issue = [&](int t0_in, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
+        const int t0 = __builtin_amdgcn_readfirstlane(t0_in);
+        // constant address space: the page table is not written while the kernel runs,
+        // so the entry is a scalar load whatever else the kernel stores
+        const long long phys = reinterpret_cast<const __attribute__((address_space(4))) int*>(
+            reinterpret_cast<uintptr_t>(pt))[t0 >> kPageShift];
         const char* kbase = p.pool + (phys * p.page_elems + head_off +
                                       static_cast<long long>(t0 & (kPageTokens - 1)) * D) * ESZ;
         // one buffer resource over the step's K rows and V rows (both planes of the page):
@@ -190,8 +200,8 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
         for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
     }
 
-    auto compute = [&](int st, const U32x4 (&kb)[UMAX][NC], const U32x4 (&vb)[UMAX][NC]) {
-        const int t0 = step_t0(st) + row_in_step;
+    auto compute = [&](int t_step, const U32x4 (&kb)[UMAX][NC], const U32x4 (&vb)[UMAX][NC]) {
+        const int t0 = t_step + row_in_step;
         float s[UMAX][GMAX];
 #pragma unroll
         for (int u = 0; u < UMAX; ++u) {
@@ -246,27 +256,30 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
         }
     };
 
-    // ---- software-pipelined stream over the split.  Every step issues the same
-    // number of loads (past the end it re-reads the step just computed, which
-    // L2 still holds), so the compiler's load counting stays exact and each
-    // step waits only for its own loads.
-    issue(0, kbuf[0], vbuf[0]);
     // ---- query slice of this lane, pre-scaled into log2 units (loaded after the
     // first K/V step is in flight, so the two latencies overlap)
-    const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
+    auto load_q = [&]() {
+        const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g)
+        for (int g = 0; g < GMAX; ++g)
 #pragma unroll
-        for (int j = 0; j < NC; ++j)
+            for (int j = 0; j < NC; ++j)
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) {
-                const int dim = (sub + LPT * j) * EPC + e;
-                const int h = min(h0 + g, p.heads - 1);  // rows past the unit's heads are read, then zeroed
-                q[g][j * EPC + e] = chunk_on[j] ? qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f) : 0.f;
-            }
+                for (int e = 0; e < EPC; ++e) {
+                    const int dim = (sub + LPT * j) * EPC + e;
+                    const int h = min(h0 + g, p.heads - 1);  // rows past the unit's heads are read, then zeroed
+                    q[g][j * EPC + e] = chunk_on[j] ? qb[static_cast<size_t>(h) * D + dim] * ((g < G) ? p.qscale : 0.f) : 0.f;
+                }
+    };
 
+    // ---- software-pipelined stream.  Every step issues the same number of loads
+    // (past the end it re-reads the step just computed, which L2 still holds), so
+    // the compiler's load counting stays exact and each step waits only for its own
+    // loads.
+    issue(step_t0(0), kbuf[0], vbuf[0]);
+    load_q();
 #pragma unroll
-    for (int i = 1; i < kPrefetch; ++i) issue(min(i, nsteps - 1), kbuf[i], vbuf[i]);
+    for (int i = 1; i < kPrefetch; ++i) issue(step_t0(min(i, nsteps - 1)), kbuf[i], vbuf[i]);
     // Unrolled by the buffer count so every buffer index is a constant: step s0 + k is
     // computed from buffer k while step s0 + k + kPrefetch is loaded into the buffer
     // computed last (past the end, the step being computed is loaded again).  Exits only
@@ -275,12 +288,12 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
 #pragma unroll
         for (int k = 0; k < kStreamBuffers; ++k) {
             const int ahead = s0 + k + kPrefetch;
-            issue(ahead < nsteps ? ahead : s0 + k, kbuf[(k + kPrefetch) % kStreamBuffers],
+            issue(step_t0(ahead < nsteps ? ahead : s0 + k), kbuf[(k + kPrefetch) % kStreamBuffers],
                   vbuf[(k + kPrefetch) % kStreamBuffers]);
             // the loads leave before any use of the step being computed, so that waiting
             // for that step never holds back the next one
             __builtin_amdgcn_sched_barrier(0);
-            compute(s0 + k, kbuf[k], vbuf[k]);
+            compute(step_t0(s0 + k), kbuf[k], vbuf[k]);
             if (s0 + k + 1 >= nsteps) goto streamed;
         }
     }
@@ -321,7 +334,6 @@ streamed:
     }
     __syncthreads();
 
-    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
     const size_t row_base = static_cast<size_t>(b) * p.heads;
     for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
         const int g = idx / D;
