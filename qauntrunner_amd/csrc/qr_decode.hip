@@ -838,9 +838,11 @@ DecodePlan plan_decode(const DecodeArgs& a) {
         work += static_cast<long long>(pages) * pl.units;
     }
     // about one workgroup per CU, whole pages per split, at most 16 pages per split
-    // (measured on MI355X: fewer, longer splits beat more resident workgroups)
+    // (measured on MI355X: fewer, longer splits beat more resident workgroups -- also on
+    // the MFMA path, whose registers allow two workgroups per CU: planning for two
+    // per CU cost 2 us at the 8B 32K fp16 shape and at the 70B 128K decode)
     (void)blocks_per_cu;
-    const int slots = cu_count() * (uses_mfma(a) ? kMfmaWgPerCu : 1);
+    const int slots = cu_count();
     long long pps = std::max<long long>(1, work / slots);
     pps = std::min<long long>(pps, 16);
     pps = std::max<long long>(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
