@@ -138,6 +138,14 @@ int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, flo
  * on one cache must be ordered by the caller (one stream, or synchronised). */
 int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_dev, float* q_dev,
                                const float* k_dev, const float* v_dev, float theta, void* stream);
+/* Same for the nq consecutive positions *pos0_dev .. *pos0_dev + nq - 1 of a chunk
+ * (prompt chunk or draft tokens, StreamingEngine.cs:831-836 / SpeculativeRunner.cs:85-93
+ * append each of them in turn): q_dev [nq][heads*head_dim], k_dev/v_dev
+ * [nq][kv_heads*head_dim].  The pages up to the last position are claimed; positions
+ * reaching past max_seq skip the append and are reported as above. */
+int qr_kv_append_rope_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, const int* pos0_dev,
+                                     float* q_dev, const float* k_dev, const float* v_dev, float theta,
+                                     void* stream);
 
 /* Attention(layer, pos, q, attn, scale), PagedKvCache.cs:83-136:
  * attn[h*D:(h+1)*D] = softmax(q_h . K[0..pos, kvh(h)] * scale) . V[0..pos, kvh(h)],
@@ -148,9 +156,9 @@ int qr_kv_attention(qr_kv* kv, int seq_id, int layer, int pos, const float* q, f
 /* Attention (PagedKvCache.cs:83-136) for n <= 64 entries whose positions are read on
  * the device, entry i over sequence seq_ids[i] at position pos_dev[i] (device int32
  * array): the companion of qr_kv_append_rope_step_dev for captured decode steps.  The
- * split plan is the one for max_seq (work past a position exits at once); the split
- * workspace can only grow outside a capture, so make one call before capturing.
- * Positions never appended read undefined values, as in the reference. */
+ * split count is planned for max_seq and each entry's positions spread over it on the
+ * device; the split workspace can only grow outside a capture, so make one call before
+ * capturing.  Positions never appended read undefined values, as in the reference. */
 int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev,
                              const float* q_dev, float* attn_dev, float scale, void* stream);
 
@@ -187,6 +195,15 @@ int qr_kv_attention_chunk(qr_kv* kv, int seq_id, int layer, int pos0, int nq, co
 int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq,
                               const void* q_dev, int q_dtype, float* attn_dev, float scale,
                               void* stream);
+/* Same with the position of query 0 read on the device from *pos0_dev (clamped to
+ * [0, max_seq - nq]): the companion of qr_kv_append_rope_chunk_step_dev for captured
+ * prefill / verify steps.  The split count is planned for max_seq and the keys of the
+ * chunk spread over it on the device; the workspace grows only outside a capture (make
+ * one call before capturing).  Caches without the MFMA chunk path (fp32, or head sizes
+ * other than 64 / 128) take fp32 queries and at most 64 of them. */
+int qr_kv_attention_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, const int* pos0_dev,
+                                   const void* q_dev, int q_dtype, float* attn_dev, float scale,
+                                   void* stream);
 
 /* Benchmark instrumentation, no reference counterpart: when `event` (a
  * hipEvent_t) is not NULL, every later attention call records it on its

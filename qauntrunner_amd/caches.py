@@ -215,6 +215,19 @@ class PagedKvCache:
         check(self._lib.qr_kv_append_rope_step_dev(self._h, seq_id, layer, pp, qp, kp, vp, theta,
                                                    _stream_ptr(stream)))
 
+    def AppendRopeChunkStepDev(self, layer, pos0_dev, q_rows, k_rows, v_rows, theta, seq_id=0,
+                               stream=None) -> None:
+        """AppendRopeStepDev of nq consecutive positions from pos0_dev (int32 [1]) on: q
+        [nq, heads*head_dim] (rotated in place, or None), k/v [nq, kv_heads*head_dim]."""
+        f32 = _lib.DTYPE_F32
+        nq = _rows_of(k_rows, self.KvDim, "k rows")
+        pp = _dev_int32(pos0_dev, 1, "pos0")
+        qp = _dev_tensor(q_rows, nq * self.Heads * self.HeadDim, f32, "q rows", allow_none=True)
+        kp = _dev_tensor(k_rows, nq * self.KvDim, f32, "k rows")
+        vp = _dev_tensor(v_rows, nq * self.KvDim, f32, "v rows")
+        check(self._lib.qr_kv_append_rope_chunk_step_dev(self._h, seq_id, layer, nq, pp, qp, kp, vp, theta,
+                                                         _stream_ptr(stream)))
+
     def Reset(self, seq_id=-1) -> None:  # PagedKvCache.cs:72
         check(self._lib.qr_kv_reset(self._h, seq_id))
 
@@ -268,8 +281,8 @@ class PagedKvCache:
 
     def AttentionStepDev(self, layer, seq_ids, pos_dev, q, out, scale, stream=None) -> None:
         """AttentionDev with the positions read on the GPU from pos_dev (int32, one per entry):
-        entry i attends positions 0..pos_dev[i] (graph-capturable; the split plan is the one
-        for max_seq)."""
+        entry i attends positions 0..pos_dev[i] (graph-capturable; the split count is planned
+        for max_seq and each entry spreads over it on the device)."""
         ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
         rows = ids.size * self.Heads * self.HeadDim
         pp = _dev_int32(pos_dev, ids.size, "pos")
@@ -310,6 +323,18 @@ class PagedKvCache:
         op = _dev_tensor(out, nq * row, _lib.DTYPE_F32, "out")
         check(self._lib.qr_kv_attention_chunk_dev(self._h, seq_id, layer, pos0, nq, qp, code, op, scale,
                                                   _stream_ptr(stream)))
+
+    def AttentionChunkStepDev(self, layer, pos0_dev, q, out, scale, q_dtype="f32", seq_id=0, stream=None) -> None:
+        """AttentionChunkDev with the position of query 0 read on the GPU from pos0_dev (int32
+        [1]); graph-capturable like AttentionStepDev."""
+        row = self.Heads * self.HeadDim
+        code = dtype_code(q_dtype)
+        nq = _rows_of(q, row, "q")
+        pp = _dev_int32(pos0_dev, 1, "pos0")
+        qp = _dev_tensor(q, nq * row, code, "q")
+        op = _dev_tensor(out, nq * row, _lib.DTYPE_F32, "out")
+        check(self._lib.qr_kv_attention_chunk_step_dev(self._h, seq_id, layer, nq, pp, qp, code, op, scale,
+                                                       _stream_ptr(stream)))
 
     # ---- debug copy-out
     def Read(self, layer, pos0, n, seq_id=0):

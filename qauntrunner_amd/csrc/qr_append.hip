@@ -130,6 +130,7 @@ __device__ __forceinline__ void v_tile_store(const AppendArgs& g, int pos0, int 
     const int T = v_tile_tokens(D, TPT);
     const int kvh = vb % g.geom.kv_heads;
     const int tbase = (pos0 / T + vb / g.geom.kv_heads) * T;
+    if (tbase >= pos0 + g.n) return;  // a tile past the rows (device positions launch the most tiles n rows can span)
     const int dp = threadIdx.x & (pairs - 1);
     const int t0 = tbase + (threadIdx.x / pairs) * TPT;
     const float* src = static_cast<const float*>(g.src[1]) + kvh * D + 2 * dp;
@@ -175,9 +176,9 @@ template <int IPT, int TPT>
 __global__ void __launch_bounds__(kRopeThreads) rope_append_items_kernel(const RopeAppendArgs a, int nv) {
     const AppendArgs& g = a.app;
     int pos0 = g.pos0;
-    if (g.pos_dev) {  // device-side position: written only where its page was claimed
+    if (g.pos_dev) {  // device-side position: written only where the pages of all rows were claimed
         pos0 = *g.pos_dev;
-        if (pos0 < 0 || pos0 >= g.max_seq || (pos0 >> kPageShift) >= *g.held_dev) return;
+        if (pos0 < 0 || pos0 > g.max_seq - g.n || ((pos0 + g.n - 1) >> kPageShift) >= *g.held_dev) return;
     }
     if (TPT > 0 && static_cast<int>(blockIdx.x) < nv) {
         v_tile_store<TPT ? TPT : 8>(g, pos0, blockIdx.x);
@@ -332,11 +333,11 @@ hipError_t launch_append(const AppendArgs& a, hipStream_t stream) {
 __global__ void __launch_bounds__(64) page_claim_kernel(const PageClaimArgs a) {
     if (threadIdx.x != 0) return;
     const int pos = *a.pos_dev;
-    if (pos < 0 || pos >= a.max_seq) {
+    if (pos < 0 || pos > a.max_seq - a.n) {
         atomicOr(&a.state[1], 2);
         return;
     }
-    const int need = (pos >> kPageShift) + 1;
+    const int need = ((pos + a.n - 1) >> kPageShift) + 1;
     const int held = a.state[a.held_index];
     if (need > held) {
         const int cnt = need - held;
@@ -349,7 +350,7 @@ __global__ void __launch_bounds__(64) page_claim_kernel(const PageClaimArgs a) {
         for (int i = 0; i < cnt; ++i) a.page_table[held + i] = first + i;
         a.state[a.held_index] = need;
     }
-    atomicMax(&a.state[a.seq_index], pos + 1);  // PagedKvCache.cs:68
+    atomicMax(&a.state[a.seq_index], pos + a.n);  // PagedKvCache.cs:68
 }
 
 hipError_t launch_page_claim(const PageClaimArgs& a, hipStream_t stream) {
@@ -366,7 +367,6 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
-    if (a.app.pos_dev && a.app.n != 1) return hipErrorInvalidValue;  // one device-side position
     const int D = a.app.geom.head_dim;
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
     const int ipt = (heads * (D / 8) + kRopeThreads - 1) / kRopeThreads;
@@ -376,7 +376,9 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     int nv = 0;
     if (tiles) {
         const int T = v_tile_tokens(D, kVTileTpt);
-        nv = ((a.app.pos0 + a.app.n - 1) / T - a.app.pos0 / T + 1) * a.app.geom.kv_heads;
+        // with a device position, the most tiles n rows can span (those past the rows return)
+        nv = (a.app.pos_dev ? (a.app.n + T - 2) / T + 1 : (a.app.pos0 + a.app.n - 1) / T - a.app.pos0 / T + 1) *
+             a.app.geom.kv_heads;
     }
     const dim3 grid(static_cast<unsigned>(a.app.n + nv));
 #define QR_ROPE_ITEMS(I)                                                                               \
@@ -403,6 +405,19 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
 hipError_t launch_widen(const void* src, int src_dtype, float* dst, long long n, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(widen_kernel, dim3(grid_for(n)), dim3(256), 0, stream, src, src_dtype, dst, n);
+    return hipGetLastError();
+}
+
+namespace {
+__global__ void __launch_bounds__(64) positions_kernel(int* out, const int* pos0_dev, int n) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (i < n) out[i] = *pos0_dev + i;
+}
+}  // namespace
+
+hipError_t launch_positions(int* out, const int* pos0_dev, int n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(positions_kernel, dim3((n + 63) / 64), dim3(64), 0, stream, out, pos0_dev, n);
     return hipGetLastError();
 }
 

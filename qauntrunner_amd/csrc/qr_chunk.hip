@@ -52,6 +52,7 @@ struct ChunkK {
     int group;
     int group_shift;         // log2(group)
     int pos0;
+    const int* pos0_dev;     // device position of query 0 (clamped to [0, pos0]) when set
     int nq;
     int q_dtype;
     const void* q;           // [nq][heads][D]
@@ -66,6 +67,23 @@ struct ChunkK {
     int units;               // splits x qblocks x kv_heads
     int per_xcd;             // launch slots per XCD: ceil(units / 8)
 };
+
+// Position of query 0: the argument, or the device-side one bounded by it (a scalar load:
+// no kernel here writes it).
+__device__ __forceinline__ int chunk_pos0(const ChunkK& p) {
+    if (!p.pos0_dev) return p.pos0;
+    const int v = reinterpret_cast<const __attribute__((address_space(4))) int*>(
+        reinterpret_cast<uintptr_t>(p.pos0_dev))[0];
+    return __builtin_amdgcn_readfirstlane(min(max(v, 0), p.pos0));
+}
+
+// Keys per split: the plan's; with a device position (the plan was made for the bound)
+// the keys of the last query spread over the planned splits, whole tiles per split.
+__device__ __forceinline__ int chunk_split_tokens(const ChunkK& p, int pos0) {
+    if (!p.pos0_dev) return p.split_tokens;
+    const int tiles = (pos0 + p.nq + kTile - 1) / kTile;
+    return (tiles + p.splits - 1) / p.splits * kTile;
+}
 
 // BF16: cache element type; NT: 16-row N tiles per wave; NSTAGE: LDS tile buffers;
 // QSPLIT: q is not exact in the cache type and enters as hi + lo parts.
@@ -114,10 +132,12 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
         row_on[j] = row_q[j] < p.nq && (rho >> p.group_shift) < p.queries_per_block;
     }
     const int q_last = min(p.nq, q_first + p.queries_per_block) - 1;
-    const int t_begin = split * p.split_tokens;
-    const int t_end = min(t_begin + p.split_tokens, p.pos0 + q_last + 1);  // causal bound of the block
+    const int pos0 = chunk_pos0(p);
+    const int split_tokens = chunk_split_tokens(p, pos0);
+    const int t_begin = split * split_tokens;
+    const int t_end = min(t_begin + split_tokens, pos0 + q_last + 1);  // causal bound of the block
     const int ntiles = t_end > t_begin ? (t_end - t_begin + kTile - 1) / kTile : 0;
-    const int unmasked_end = p.pos0 + q_first + 1;  // positions below it are seen by every row
+    const int unmasked_end = pos0 + q_first + 1;  // positions below it are seen by every row
 
     // ---- DMA of tile `it` into stage it % NSTAGE.  K: row t of the tile at t*RB, its
     // chunk c at slot c ^ fk(t); V^T: dim row d at KB + 128 d, chunk c (positions
@@ -260,7 +280,7 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
         if (t0 + kTile > unmasked_end || t0 + kTile > t_end) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                const int lim = min(t_end - 1, p.pos0 + row_q[j]);  // last position row j sees
+                const int lim = min(t_end - 1, pos0 + row_q[j]);  // last position row j sees
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -458,6 +478,7 @@ hipError_t launch_chunk(const ChunkArgs& a, const ChunkPlan& pl, void* workspace
     while ((1 << gs) < k.group) ++gs;
     k.group_shift = gs;
     k.pos0 = a.pos0;
+    k.pos0_dev = a.pos0_dev;
     k.nq = a.nq;
     k.q_dtype = a.q_dtype;
     k.q = a.q;

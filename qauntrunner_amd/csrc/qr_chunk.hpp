@@ -12,6 +12,9 @@ struct ChunkArgs {
     int kv_dtype;           // F16 or BF16
     int heads;
     int pos0;               // position of query 0
+    // Device-side position of query 0: when set the kernels read it, clamped to [0, pos0];
+    // pos0 is then the largest position query 0 may take, which the plan is made for.
+    const int* pos0_dev;
     int nq;
     const void* q;          // device [nq][heads][head_dim] in q_dtype
     int q_dtype;

@@ -86,6 +86,16 @@ __device__ __forceinline__ int entry_seq(const DecodeK& p, int b) {
     return __builtin_amdgcn_readfirstlane(min(max(pos + 1, 1), p.seq_len[b]));
 }
 
+// Positions per split of an entry attending `seq` positions: the plan's; with device
+// positions (the plan was made for the bound) the entry's pages spread over the planned
+// splits instead, so a short sequence still spreads over the GPU.  Never more than the
+// plan's (the partials buffer holds split_stride splits).
+__device__ __forceinline__ int entry_split_tokens(const DecodeK& p, int seq) {
+    if (!p.pos_dev) return p.split_tokens;
+    const int pages = (seq + kPageTokens - 1) >> kPageShift;
+    return ((pages + p.split_stride - 1) / p.split_stride) << kPageShift;
+}
+
 __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
 }
@@ -103,10 +113,11 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     const int unit = blockIdx.y;
     const int b = blockIdx.z;
     const int seq = entry_seq(p, b);
-    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    const int split_tokens = entry_split_tokens(p, seq);
+    const int nsplit = (seq + split_tokens - 1) / split_tokens;
     if (split >= nsplit) return;
-    const int t_begin = split * p.split_tokens;
-    const int t_end = min(seq, t_begin + p.split_tokens);
+    const int t_begin = split * split_tokens;
+    const int t_end = min(seq, t_begin + split_tokens);
 
     const int D = DT ? DT : p.head_dim;
     const int lsh = DT ? __builtin_ctz(DT / DPL) : p.lpt_shift;
@@ -403,9 +414,10 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     const int unit = blockIdx.y;
     const int b = blockIdx.z;
     const int seq = entry_seq(p, b);
-    const int t_begin = split * p.split_tokens;
+    const int split_tokens = entry_split_tokens(p, seq);
+    const int t_begin = split * split_tokens;
     if (t_begin >= seq) return;
-    const int t_end = min(seq, t_begin + p.split_tokens);
+    const int t_end = min(seq, t_begin + split_tokens);
     const int lane = threadIdx.x & 63;
     // wave-uniform (SGPR): step positions, and so the page-table entry of a step, are
     // scalar; a vector load there would make every step wait for all loads in flight
@@ -590,7 +602,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         sm_l[wave][n] = l;
     }
     __syncthreads();
-    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    const int nsplit = (seq + split_tokens - 1) / split_tokens;
     const size_t row_base = static_cast<size_t>(b) * p.heads;
     for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
         const int g = idx / D;
@@ -625,7 +637,8 @@ __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK 
     const int h = blockIdx.x;
     const int b = blockIdx.y;
     const int seq = entry_seq(p, b);
-    const int nsplit = (seq + p.split_tokens - 1) / p.split_tokens;
+    const int split_tokens = entry_split_tokens(p, seq);
+    const int nsplit = (seq + split_tokens - 1) / split_tokens;
     if (nsplit <= 1) return;
     const int D = p.head_dim;
     const size_t base = (static_cast<size_t>(b) * p.heads + h) * p.split_stride;

@@ -47,19 +47,19 @@ struct AppendArgs {
     int src_dtype;
     int pos0;
     int n;
-    // Device-side position (single-position appends): when set, pos0 is *pos_dev, read
-    // by the kernel, and the row is written only if the page of that position is held
-    // (*held_dev pages) and the position lies in [0, max_seq).
+    // Device-side position (RoPE appends): when set, pos0 is *pos_dev, read by the
+    // kernel, and the n rows are written only if the page of the last is held (*held_dev
+    // pages) and positions pos0 .. pos0 + n - 1 lie in [0, max_seq).
     const int* pos_dev;
     const int* held_dev;
     int max_seq;
 };
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
 
-// Device-side page claim for one appended position read from *pos_dev: pages
-// held..(pos >> 8) of one (sequence, layer) get the next indices of the pool's
-// device counter and their page-table entries; SeqLen's device copy grows to pos + 1.
-// state: [0] pages handed out, [1] error bits (1: pool full, 2: position outside
+// Device-side page claim for n appended positions from *pos_dev on: pages
+// held..((pos + n - 1) >> 8) of one (sequence, layer) get the next indices of the pool's
+// device counter and their page-table entries; SeqLen's device copy grows to pos + n.
+// state: [0] pages handed out, [1] error bits (1: pool full, 2: positions outside
 // [0, max_seq)), then `held` and `seq_len` entries at the given indices.
 struct PageClaimArgs {
     int* page_table;   // entries of this (sequence, layer)
@@ -68,7 +68,8 @@ struct PageClaimArgs {
     int seq_index;     // index of the sequence's SeqLen in state
     int capacity;      // pages in the pool
     int max_seq;
-    const int* pos_dev;
+    const int* pos_dev;  // first position of the rows
+    int n;               // rows: positions pos .. pos + n - 1
 };
 hipError_t launch_page_claim(const PageClaimArgs& a, hipStream_t stream);
 
@@ -102,6 +103,9 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream);
 
 // Widens 16-bit rows to fp32 (exact) -- used for 16-bit query inputs.
 hipError_t launch_widen(const void* src, int src_dtype, float* dst, long long n, hipStream_t stream);
+
+// out[i] = *pos0_dev + i for i < n (device positions of the queries of a chunk).
+hipError_t launch_positions(int* out, const int* pos0_dev, int n, hipStream_t stream);
 
 // ------------------------------------------------------------------ GQA decode
 constexpr int kMaxDecodeBatch = 64;  // decode entries per launch (descriptor passed by value)

@@ -23,6 +23,7 @@ struct qr_kv {
     hipStream_t stream = nullptr;
     DevBuf stage;      // host <-> device staging of rows, queries and outputs
     DevBuf workspace;  // split-K partials
+    DevBuf steppos;    // device positions of the queries of a device-position chunk (kMaxDecodeBatch ints)
     hipEvent_t split_event = nullptr;  // benchmark instrumentation (qr_kv_set_split_event)
     void* scratch = nullptr;           // this device's decode scratch array (no-allocation calls)
     bool device_steps = false;         // the device copy of the page accounting is in use
@@ -237,6 +238,7 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
         st = kv->store.init(g, kv_dtype, layers, max_batch, max_seq);
     }
     if (st == QR_OK) st = decode_scratch_address(kv->device, &kv->scratch);
+    if (st == QR_OK) st = kv->steppos.ensure(kMaxDecodeBatch * sizeof(int));
     if (st == QR_OK && hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed");
         st = QR_ERR_HIP;
@@ -647,14 +649,27 @@ int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, v
     return QR_OK;
 }
 
-int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_dev, float* q_dev,
-                               const float* k_dev, const float* v_dev, float theta, void* stream) {
-    clear_error();
-    QR_TRY(check_handle(kv));
+}  // extern "C"
+
+namespace {
+
+// The split workspace may only grow outside stream capture.
+int grow_workspace(qr_kv* kv, size_t bytes, hipStream_t st) {
+    const size_t ws = std::max<size_t>(bytes, 256);
+    if (ws > kv->workspace.size()) {
+        QR_CHECK_ARG(!capturing(st), "the split workspace must grow to %zu bytes: make one call outside capture first", ws);
+        QR_TRY(kv->workspace.ensure(ws));
+    }
+    return QR_OK;
+}
+
+// Ensure + RoPE + Append of n rows at the device positions *pos_dev .. *pos_dev + n - 1
+// (the single-position and the chunk step calls).
+int rope_step_dev(qr_kv* kv, int seq_id, int layer, int n, const int* pos_dev, float* q_dev, const float* k_dev,
+                  const float* v_dev, float theta, hipStream_t st) {
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(pos_dev && k_dev && v_dev, "null pos/k/v pointer");
     DeviceGuard dg(kv->device);
-    const hipStream_t st = as_stream(stream);
     const bool cap = capturing(st);
     if (!kv->device_steps) {
         // first device-side append: the device copy starts from the host accounting
@@ -675,6 +690,7 @@ int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_
     c.capacity = static_cast<int>(std::min<long long>(kv->store.capacity(), 0x7FFFFFFF));
     c.max_seq = kv->max_seq;
     c.pos_dev = pos_dev;
+    c.n = n;
     QR_HIP(launch_page_claim(c, st));
     RopeAppendArgs a{};
     a.app.pool = kv->store.pool();
@@ -688,7 +704,7 @@ int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_
     a.app.src_stride = kv->kv_dim;
     a.app.src_dtype = QR_DTYPE_F32;
     a.app.pos0 = 0;
-    a.app.n = 1;
+    a.app.n = n;
     a.app.pos_dev = pos_dev;
     a.app.held_dev = kv->store.state_dev() + c.held_index;
     a.app.max_seq = kv->max_seq;
@@ -701,16 +717,9 @@ int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_
     return QR_OK;
 }
 
-int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev,
-                             const float* q_dev, float* attn_dev, float scale, void* stream) {
-    clear_error();
-    QR_TRY(check_handle(kv));
-    QR_CHECK_ARG(q_dev && attn_dev && pos_dev, "null q/attn/pos pointer");
-    QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for device positions", n,
-                 kMaxDecodeBatch);
-    QR_CHECK_ARG(seq_ids, "null seq_ids array");
-    DeviceGuard dg(kv->device);
-    const hipStream_t st = as_stream(stream);
+// Decode where entry i attends positions 0..pos_dev[i] (read on the device).
+int attention_step(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev, const float* q_dev,
+                   float* attn_dev, float scale, hipStream_t st) {
     QR_CHECK_ARG(kv->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
     DecodeArgs a{};
     for (int i = 0; i < n; ++i) {
@@ -729,13 +738,80 @@ int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, co
     a.nb = n;
     a.pos_dev = pos_dev;
     const DecodePlan plan = plan_decode(a);
-    const size_t ws = std::max<size_t>(plan.workspace_bytes, 256);
-    if (ws > kv->workspace.size()) {
-        QR_CHECK_ARG(!capturing(st), "the split workspace must grow to %zu bytes: make one call outside capture first", ws);
-        QR_TRY(kv->workspace.ensure(ws));
-    }
+    QR_TRY(grow_workspace(kv, plan.workspace_bytes, st));
     QR_HIP(launch_decode(a, plan, kv->workspace.get(), st, nullptr));
     return QR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_kv_append_rope_step_dev(qr_kv* kv, int seq_id, int layer, const int* pos_dev, float* q_dev,
+                               const float* k_dev, const float* v_dev, float theta, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    return rope_step_dev(kv, seq_id, layer, 1, pos_dev, q_dev, k_dev, v_dev, theta, as_stream(stream));
+}
+
+int qr_kv_append_rope_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, const int* pos0_dev, float* q_dev,
+                                     const float* k_dev, const float* v_dev, float theta, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(nq >= 1 && nq <= kv->max_seq, "nq %d outside [1, %d]", nq, kv->max_seq);
+    return rope_step_dev(kv, seq_id, layer, nq, pos0_dev, q_dev, k_dev, v_dev, theta, as_stream(stream));
+}
+
+int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos_dev,
+                             const float* q_dev, float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_CHECK_ARG(q_dev && attn_dev && pos_dev, "null q/attn/pos pointer");
+    QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for device positions", n,
+                 kMaxDecodeBatch);
+    QR_CHECK_ARG(seq_ids, "null seq_ids array");
+    DeviceGuard dg(kv->device);
+    return attention_step(kv, n, seq_ids, layer, pos_dev, q_dev, attn_dev, scale, as_stream(stream));
+}
+
+int qr_kv_attention_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, const int* pos0_dev, const void* q_dev,
+                                   int q_dtype, float* attn_dev, float scale, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(kv));
+    QR_TRY(check_seq_layer(kv, seq_id, layer));
+    QR_CHECK_ARG(q_dev && attn_dev && pos0_dev, "null q/attn/pos pointer");
+    QR_CHECK_ARG(dtype_valid(q_dtype), "unknown q dtype %d", q_dtype);
+    QR_CHECK_ARG(nq >= 1 && nq <= kv->max_seq, "nq %d outside [1, %d]", nq, kv->max_seq);
+    DeviceGuard dg(kv->device);
+    const hipStream_t st = as_stream(stream);
+    QR_CHECK_ARG(kv->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
+    if (chunk_mfma_eligible(kv->dtype, kv->head_dim, kv->heads, kv->kv_heads)) {
+        ChunkArgs c{};
+        c.pool = kv->store.pool();
+        c.page_table = kv->store.page_table_dev() + kv->store.pt_offset(seq_id, layer);
+        c.geom = kv->store.geom();
+        c.kv_dtype = kv->dtype;
+        c.heads = kv->heads;
+        c.pos0 = kv->max_seq - nq;  // bound of the plan; the kernels read the position
+        c.pos0_dev = pos0_dev;
+        c.nq = nq;
+        c.q = q_dev;
+        c.q_dtype = q_dtype;
+        c.out = attn_dev;
+        c.scale = scale;
+        const ChunkPlan plan = plan_chunk(c);
+        QR_TRY(grow_workspace(kv, plan.workspace_bytes, st));
+        QR_HIP(launch_chunk(c, plan, kv->workspace.get(), st, nullptr));
+        return QR_OK;
+    }
+    // other caches: one decode entry per query, its position written on the device
+    QR_CHECK_ARG(q_dtype == QR_DTYPE_F32, "device-position chunks on this cache take fp32 queries (got dtype %d)", q_dtype);
+    QR_CHECK_ARG(nq <= kMaxDecodeBatch, "device-position chunks on this cache take at most %d queries (got %d)",
+                 kMaxDecodeBatch, nq);
+    int* pos = static_cast<int*>(kv->steppos.get());
+    QR_HIP(launch_positions(pos, pos0_dev, nq, st));
+    const std::vector<int> ids(nq, seq_id);
+    return attention_step(kv, nq, ids.data(), layer, pos, static_cast<const float*>(q_dev), attn_dev, scale, st);
 }
 
 }  // extern "C"

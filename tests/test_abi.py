@@ -76,6 +76,10 @@ def test_null_handles_are_rejected():
     assert L.qr_mla_set_rope(None, 64) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_append_rope_step_dev(None, 0, 0, None, None, None, None, 1e4, None) == _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_attention_step_dev(None, 1, None, 0, None, None, None, 1.0, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_append_rope_chunk_step_dev(None, 0, 0, 4, None, None, None, None, 1e4, None) == \
+        _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_kv_attention_chunk_step_dev(None, 0, 0, 4, None, None, 0, None, 1.0, None) == \
+        _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_destroy(None) == 0 and L.qr_mla_destroy(None) == 0
     assert "null" in L.qr_last_error().decode() or L.qr_last_error() == b""
 

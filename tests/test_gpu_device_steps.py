@@ -176,3 +176,142 @@ def test_captured_decode_step_replays_at_advancing_positions(gpu, dtype):
             ka, va = A.Read(layer, 0, p0 + steps + 1)
             kb, vb = B.Read(layer, 0, p0 + steps + 1)
             assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_decode_step_spreads_short_sequences_over_the_planned_splits(gpu, dtype):
+    """max_seq 131072 bounds the plan (many splits); entries at 3,000 and 9,000 positions
+    spread over them on the device and agree with the host-planned call."""
+    import torch
+
+    heads, kv_heads, D, max_seq = 8, 2, 128, 131072
+    n = 9001
+    Q, K, V = _rows(900, n, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, max_seq, kv_dtype=dtype, max_batch=2) as kv:
+        for s in range(2):
+            kv.AppendRangeDev(0, 0, dev(K), dev(V), seq_id=s)
+        ids, pos = [0, 1], [2999, 9000]
+        q = dev(Q[:2])
+        want = torch.empty_like(q)
+        kv.AttentionDev(0, ids, pos, q, want, scale)
+        got = torch.empty_like(q)
+        kv.AttentionStepDev(0, ids, torch.tensor(pos, dtype=torch.int32, device=gpu), q, got, scale)
+        torch.cuda.synchronize()
+        w, g = want.cpu().numpy(), got.cpu().numpy()
+        tol = (2e-6 if dtype == "f32" else 1e-5) * float(np.max(np.abs(w)))
+        assert float(np.max(np.abs(g - w))) <= tol
+
+
+def _chunk_host_step(kv, layer, p0, q, k, v, out):
+    """Host-position reference: rotates q in place, appends k/v, causal attention of the chunk."""
+    kv.AppendRopeDev(layer, p0, q, k, v, THETA)
+    kv.AttentionChunkDev(layer, p0, q, out, 1.0 / np.sqrt(kv.HeadDim))
+
+
+@pytest.mark.parametrize("dtype,max_seq", [("f16", 4096), ("f16", 65536), ("f32", 4096)])
+def test_chunk_steps_match_the_host_path(gpu, dtype, max_seq):
+    """qr_kv_append_rope_chunk_step_dev + qr_kv_attention_chunk_step_dev against the host-
+    position chunk calls: 16-bit caches take the MFMA chunk kernel (its keys spread over the
+    splits planned for max_seq), fp32 caches one decode entry per query."""
+    import torch
+
+    heads, kv_heads, D = 8, 2, 128
+    p0, nq = 250, 12  # the chunk crosses the page boundary at 256
+    Q, K, V = _rows(1000, p0 + 2 * nq, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    with qr.PagedKvCache(1, heads, kv_heads, D, max_seq, kv_dtype=dtype) as A, \
+            qr.PagedKvCache(1, heads, kv_heads, D, max_seq, kv_dtype=dtype) as B:
+        for kv in (A, B):
+            kv.AppendRopeDev(0, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        pos0 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        for c in range(2):
+            t = p0 + c * nq
+            qa, qb = dev(Q[t:t + nq]), dev(Q[t:t + nq])
+            oa, ob = torch.empty_like(qa), torch.empty_like(qb)
+            _chunk_host_step(A, 0, t, qa, dev(K[t:t + nq]), dev(V[t:t + nq]), oa)
+            pos0.fill_(t)
+            B.AppendRopeChunkStepDev(0, pos0, qb, dev(K[t:t + nq]), dev(V[t:t + nq]), THETA)
+            B.AttentionChunkStepDev(0, pos0, qb, ob, 1.0 / np.sqrt(D))
+            torch.cuda.synchronize()
+            assert torch.equal(qa, qb), f"rotated q, chunk {c}"
+            w, g = oa.cpu().numpy(), ob.cpu().numpy()
+            tol = (2e-6 if dtype == "f32" else 1e-5) * float(np.max(np.abs(w)))
+            assert float(np.max(np.abs(g - w))) <= tol, f"attention, chunk {c}"
+        assert B.SeqLen == A.SeqLen == p0 + 2 * nq
+        assert B.BytesUsed == A.BytesUsed
+        ka, va = A.Read(0, 0, p0 + 2 * nq)
+        kb, vb = B.Read(0, 0, p0 + 2 * nq)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_captured_chunk_step_replays_at_advancing_positions(gpu, dtype):
+    """A verify-sized step (8 draft queries, append + attention, two layers) captured once
+    and replayed at advancing chunk positions across a page boundary."""
+    import torch
+
+    heads, kv_heads, D, max_seq, layers, nq = 8, 2, 128, 8192, 2, 8
+    p0, chunks = 480, 6  # 480 + 48 crosses 512
+    Q, K, V = _rows(1100, p0 + nq * (chunks + 1), heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(layers, heads, kv_heads, D, max_seq, kv_dtype=dtype) as A, \
+            qr.PagedKvCache(layers, heads, kv_heads, D, max_seq, kv_dtype=dtype) as B:
+        for kv in (A, B):
+            for layer in range(layers):
+                kv.AppendRopeDev(layer, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        B.Reserve(64)
+        pos0 = torch.zeros(1, dtype=torch.int32, device=gpu)
+        qbuf = [torch.empty(nq, heads * D, device=gpu) for _ in range(layers)]
+        kbuf, vbuf = torch.empty(nq, kv_heads * D, device=gpu), torch.empty(nq, kv_heads * D, device=gpu)
+        obuf = [torch.empty(nq, heads * D, device=gpu) for _ in range(layers)]
+
+        def step_b():
+            for layer in range(layers):
+                B.AppendRopeChunkStepDev(layer, pos0, qbuf[layer], kbuf, vbuf, THETA)
+                B.AttentionChunkStepDev(layer, pos0, qbuf[layer], obuf[layer], scale)
+
+        def load(t):
+            pos0.fill_(t)
+            kbuf.copy_(dev(K[t:t + nq]))
+            vbuf.copy_(dev(V[t:t + nq]))
+            for layer in range(layers):
+                qbuf[layer].copy_(dev(Q[t:t + nq]))
+
+        def check(t):
+            for layer in range(layers):
+                qa, oa = dev(Q[t:t + nq]), torch.empty(nq, heads * D, device=gpu)
+                _chunk_host_step(A, layer, t, qa, dev(K[t:t + nq]), dev(V[t:t + nq]), oa)
+                torch.cuda.synchronize()
+                assert torch.equal(qa, qbuf[layer]), f"rotated q, layer {layer}, chunk at {t}"
+                w, g = oa.cpu().numpy(), obuf[layer].cpu().numpy()
+                tol = (2e-6 if dtype == "f32" else 1e-5) * float(np.max(np.abs(w)))
+                assert float(np.max(np.abs(g - w))) <= tol, f"attention, layer {layer}, chunk at {t}"
+
+        load(p0)
+        step_b()  # eager first call: device accounting and split workspace
+        torch.cuda.synchronize()
+        check(p0)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            load(p0 + nq)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step_b()
+        for c in range(1, chunks + 1):
+            t = p0 + c * nq
+            load(t)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            check(t)
+        end = p0 + nq * (chunks + 1)
+        assert B.SeqLen == A.SeqLen == end
+        for layer in range(layers):
+            ka, va = A.Read(layer, 0, end)
+            kb, vb = B.Read(layer, 0, end)
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}"
