@@ -286,6 +286,23 @@ int qr_mla_attend_absorbed(qr_mla* mla, int layer, int pos, int heads, int nope,
 int qr_mla_attend_absorbed_dev(qr_mla* mla, int layer, int pos, int heads, int nope, int vdim,
                                const float* q_dev, const void* kvb_dev, int kvb_format,
                                float* out_dev, void* stream);
+/* Device-position forms, no reference counterpart (for captured decode, prefill-chunk
+ * and verify steps, as qr_kv_append_rope_step_dev / qr_kv_attention_step_dev): the n
+ * latent rows rows_dev [n][latentDim] go to positions *pos0_dev .. *pos0_dev + n - 1,
+ * their pages claimed on the device (Append, MlaLatentCache.cs:45-51); the attention and
+ * the absorbed block run at position *pos_dev, read on the device (the split count is
+ * planned for max_seq and the sequence spreads over it).  Reserve pages (qr_mla_reserve)
+ * before capturing and make the cache's first device-position call outside capture; a
+ * full pool or positions outside [0, max_seq) skip the append and are reported by the
+ * next host-side call (QR_ERR_OUT_OF_MEMORY / QR_ERR_OUT_OF_RANGE). */
+int qr_mla_append_step_dev(qr_mla* mla, int layer, int n, const int* pos0_dev, const void* rows_dev,
+                           int src_dtype, void* stream);
+int qr_mla_attention_step_dev(qr_mla* mla, int layer, const int* pos_dev, int heads,
+                              const float* q_tilde_dev, const float* q_rope_dev, float scale,
+                              float* u_dev, void* stream);
+int qr_mla_attend_absorbed_step_dev(qr_mla* mla, int layer, const int* pos_dev, int heads, int nope,
+                                    int vdim, const float* q_dev, const void* kvb_dev, int kvb_format,
+                                    float* out_dev, void* stream);
 int qr_mla_reset(qr_mla* mla);                    /* MlaLatentCache.cs:53 */
 int qr_mla_truncate(qr_mla* mla, int len);        /* MlaLatentCache.cs:57 */
 int qr_mla_seq_len(const qr_mla* mla, int* out);  /* MlaLatentCache.cs:19 */

@@ -81,6 +81,9 @@ SIGNATURES = {
     "qr_kv_attention_step_dev": [_p, _i, _p, _i, _p, _p, _p, _f, _p],
     "qr_kv_append_rope_chunk_step_dev": [_p, _i, _i, _i, _p, _p, _p, _p, _f, _p],
     "qr_kv_attention_chunk_step_dev": [_p, _i, _i, _i, _p, _p, _i, _p, _f, _p],
+    "qr_mla_append_step_dev": [_p, _i, _i, _p, _p, _i, _p],
+    "qr_mla_attention_step_dev": [_p, _i, _p, _i, _p, _p, _f, _p, _p],
+    "qr_mla_attend_absorbed_step_dev": [_p, _i, _p, _i, _i, _i, _p, _p, _i, _p, _p],
     "qr_kv_attention": [_p, _i, _i, _i, _p, _p, _f],
     "qr_kv_attention_batch": [_p, _i, _p, _i, _p, _p, _p, _f],
     "qr_kv_attention_dev": [_p, _i, _p, _i, _p, _p, _p, _f, _p],

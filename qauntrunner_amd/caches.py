@@ -494,3 +494,36 @@ class MlaLatentCache:
         up = _dev_tensor(u, heads * kv_lora, f32, "u")
         check(self._lib.qr_mla_attention_dev(self._h, layer, pos, heads, qt, qr_ptr, scale, up,
                                              _stream_ptr(stream)))
+
+    # ---- device-position forms (graph-capturable steps; pages reserved before capture)
+    def AppendStepDev(self, layer, pos0_dev, rows, src_dtype="f32", stream=None) -> None:
+        """AppendRangeDev at the positions pos0_dev[0] .. + n - 1 read on the GPU (int32 [1]);
+        their pages are claimed on the device."""
+        code = dtype_code(src_dtype)
+        n = _rows_of(rows, self.LatentDim, "latent rows")
+        pp = _dev_int32(pos0_dev, 1, "pos0")
+        rp = _dev_tensor(rows, n * self.LatentDim, code, "latent rows")
+        check(self._lib.qr_mla_append_step_dev(self._h, layer, n, pp, rp, code, _stream_ptr(stream)))
+
+    def AbsorbedAttentionStepDev(self, layer, pos_dev, q_tilde, q_rope, u, scale, stream=None) -> None:
+        """AbsorbedAttentionDev at the position read on the GPU from pos_dev (int32 [1])."""
+        f32 = _lib.DTYPE_F32
+        kv_lora, rope = self._split()
+        heads = _rows_of(q_tilde, kv_lora, "q_tilde")
+        pp = _dev_int32(pos_dev, 1, "pos")
+        qt = _dev_tensor(q_tilde, heads * kv_lora, f32, "q_tilde")
+        qr_ptr = _dev_tensor(q_rope, heads * rope, f32, "q_rope", allow_none=rope == 0)
+        up = _dev_tensor(u, heads * kv_lora, f32, "u")
+        check(self._lib.qr_mla_attention_step_dev(self._h, layer, pp, heads, qt, qr_ptr, scale, up,
+                                                  _stream_ptr(stream)))
+
+    def AttendAbsorbedStepDev(self, layer, pos_dev, q, kvb, fmt, nope, vdim, out, stream=None) -> None:
+        """AttendAbsorbedDev at the position read on the GPU from pos_dev (int32 [1])."""
+        f32 = _lib.DTYPE_F32
+        rope = self._split()[1]
+        heads = _rows_of(q, nope + rope, "q")
+        pp = _dev_int32(pos_dev, 1, "pos")
+        qp = _dev_tensor(q, heads * (nope + rope), f32, "q")
+        op = _dev_tensor(out, heads * vdim, f32, "out")
+        check(self._lib.qr_mla_attend_absorbed_step_dev(self._h, layer, pp, heads, nope, vdim, qp, _dev_ptr(kvb),
+                                                        fmt, op, _stream_ptr(stream)))

@@ -40,6 +40,11 @@ __device__ __forceinline__ long long page_offset(const PageGeom& g, long long ph
 }
 
 __global__ void __launch_bounds__(256) append_kernel(const AppendArgs a) {
+    int pos0 = a.pos0;
+    if (a.pos_dev) {  // device-side position: written only where the pages of all rows were claimed
+        pos0 = *a.pos_dev;
+        if (pos0 < 0 || pos0 > a.max_seq - a.n || ((pos0 + a.n - 1) >> kPageShift) >= *a.held_dev) return;
+    }
     const int width = a.geom.kv_heads * a.geom.head_dim;
     const long long per_plane = static_cast<long long>(a.n) * width;
     const long long total = per_plane * a.geom.planes;
@@ -50,7 +55,7 @@ __global__ void __launch_bounds__(256) append_kernel(const AppendArgs a) {
         const int r = static_cast<int>(rem / width);
         const int col = static_cast<int>(rem - static_cast<long long>(r) * width);
         if (col >= a.row_len[plane]) continue;
-        const int t = a.pos0 + r;
+        const int t = pos0 + r;
         const long long phys = a.page_table[t >> kPageShift];
         convert_store(a.pool, a.dtype, page_offset(a.geom, phys, plane, t & (kPageTokens - 1), col),
                       a.src[plane], a.src_dtype, static_cast<long long>(r) * a.src_stride + col);

@@ -47,7 +47,7 @@ struct AppendArgs {
     int src_dtype;
     int pos0;
     int n;
-    // Device-side position (RoPE appends): when set, pos0 is *pos_dev, read by the
+    // Device-side position (appends and RoPE appends): when set, pos0 is *pos_dev, read by the
     // kernel, and the n rows are written only if the page of the last is held (*held_dev
     // pages) and positions pos0 .. pos0 + n - 1 lie in [0, max_seq).
     const int* pos_dev;

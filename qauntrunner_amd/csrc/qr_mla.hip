@@ -29,6 +29,7 @@ struct MlaK {
     int kv_lora, rope, width;
     int heads;
     int seq_len;
+    const int* pos_dev;  // device position (seq = pos + 1, clamped to [1, seq_len]) when set
     int split_tokens;
     int splits;
     const float* q_tilde;
@@ -47,6 +48,15 @@ __device__ __forceinline__ float load_elem(const char* pool, int dtype, long lon
     }
 }
 
+// Positions attended: seq_len, or a device position + 1 bounded by it (a scalar load: no
+// kernel here writes positions).
+__device__ __forceinline__ int device_seq(const int* pos_dev, int seq_len) {
+    if (!pos_dev) return seq_len;
+    const int pos = reinterpret_cast<const __attribute__((address_space(4))) int*>(
+        reinterpret_cast<uintptr_t>(pos_dev))[0];
+    return __builtin_amdgcn_readfirstlane(min(max(pos + 1, 1), seq_len));
+}
+
 __device__ __forceinline__ long long row_base(const MlaK& p, int t) {
     const long long phys = p.page_table[t >> kPageShift];
     return (phys * kPageTokens + (t & (kPageTokens - 1))) * p.width;
@@ -56,8 +66,8 @@ __global__ void __launch_bounds__(kThreads) mla_split_generic_kernel(const MlaK 
     const int split = blockIdx.x;
     const int h = blockIdx.y;
     const int t0 = split * p.split_tokens;
-    const int t1 = min(p.seq_len, t0 + p.split_tokens);
-    const int n = t1 - t0;
+    const int t1 = min(device_seq(p.pos_dev, p.seq_len), t0 + p.split_tokens);
+    const int n = t1 - t0;  // <= 0 past a device position: a zero partial of weight 0
 
     __shared__ float sq[kMlaMaxLora + kMlaMaxRope];
     __shared__ float sp[kGenericSplit];
@@ -221,6 +231,7 @@ struct MlaMK {
     const int* page_table;
     int heads;
     int seq_len;
+    const int* pos_dev;  // device position (seq = pos + 1, clamped to [1, seq_len]) when set
     int split_tokens;  // multiple of kMTile
     int splits;
     int groups;        // head groups of kMHeads
@@ -232,6 +243,14 @@ struct MlaMK {
     float4* part_ml;   // [heads][splits] (m, l, e, 0)
     float qscale;      // scale * log2(e)
 };
+
+// Positions per split: the plan's; with a device position (the plan was made for the
+// bound) the tiles of the sequence spread over the planned splits.
+__device__ __forceinline__ int mla_split_tokens(const MlaMK& p, int seq) {
+    if (!p.pos_dev) return p.split_tokens;
+    const int tiles = (seq + kMTile - 1) / kMTile;
+    return (tiles + p.splits - 1) / p.splits * kMTile;
+}
 
 template <bool SRC_BF16, int KR>
 __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
@@ -268,8 +287,12 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     if (idx >= p.groups * p.splits) return;
     const int hg = idx % p.groups;
     const int split = idx / p.groups;
-    const int t_begin = split * p.split_tokens;
-    const int t_end = min(p.seq_len, t_begin + p.split_tokens);
+    const int seq = device_seq(p.pos_dev, p.seq_len);
+    const int split_tokens = mla_split_tokens(p, seq);
+    const int nsplit = (seq + split_tokens - 1) / split_tokens;
+    if (split >= nsplit) return;
+    const int t_begin = split * split_tokens;
+    const int t_end = min(seq, t_begin + split_tokens);
     const int ntiles = (t_end - t_begin + kMTile - 1) / kMTile;  // >= 1
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -565,7 +588,7 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     float l[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) l[nt] = lds_l[16 * nt + l16];
-    if (p.splits == 1) {
+    if (nsplit == 1) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int head = hg * kMHeads + 16 * nt + l16;
@@ -656,15 +679,19 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
     const size_t base = static_cast<size_t>(h) * p.splits;
     const int d = blk * 128 + c4 * 4;
     const _Float16* part = static_cast<const _Float16*>(p.part_u);
+    const int seq = device_seq(p.pos_dev, p.seq_len);
+    const int split_tokens = mla_split_tokens(p, seq);
+    const int nsplit = (seq + split_tokens - 1) / split_tokens;
+    if (nsplit == 1) return;  // the tile kernel wrote u
     float m = -INFINITY, l = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = grp; s0 < p.splits; s0 += 64) {
+    for (int s0 = grp; s0 < nsplit; s0 += 64) {
         uint2 a[8];
         float4 ml[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int s = s0 + 8 * i;
-            const bool in = s < p.splits;
+            const bool in = s < nsplit;
             a[i] = in ? *reinterpret_cast<const uint2*>(part + (base + s) * KL + d) : make_uint2(0u, 0u);
             ml[i] = in ? p.part_ml[base + s] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
         }
@@ -776,6 +803,7 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
         k.page_table = a.page_table;
         k.heads = a.heads;
         k.seq_len = a.seq_len;
+        k.pos_dev = a.pos_dev;
         k.split_tokens = pl.split_tokens;
         k.splits = pl.splits;
         k.groups = (a.heads + kMHeads - 1) / kMHeads;
@@ -816,6 +844,7 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
     k.width = a.kv_lora + a.rope;
     k.heads = a.heads;
     k.seq_len = a.seq_len;
+    k.pos_dev = a.pos_dev;
     k.split_tokens = pl.split_tokens;
     k.splits = pl.splits;
     k.q_tilde = a.q_tilde;

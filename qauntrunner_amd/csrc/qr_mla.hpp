@@ -16,7 +16,8 @@ struct MlaArgs {
     int kv_lora;
     int rope;
     int heads;
-    int seq_len;             // pos + 1
+    int seq_len;             // pos + 1 (the bound, when pos_dev is set)
+    const int* pos_dev;      // device position read by the kernels (clamped to [0, seq_len - 1]), or null
     const float* q_tilde;    // [heads][kv_lora]
     const float* q_rope;     // [heads][rope]
     float* u;                // [heads][kv_lora]

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <new>
+#include <vector>
 
 #include "qr_mla.hpp"
 #include "qr_proj.hpp"
@@ -20,6 +21,7 @@ struct qr_mla {
     DevBuf stage;
     DevBuf workspace;
     DevBuf proj;  // q_tilde, u and q_rope of the absorbed layer call
+    bool device_steps = false;  // the device copy of the page accounting is in use
 };
 
 namespace {
@@ -54,6 +56,45 @@ int check_resident(const qr_mla* m, int layer, int pos) {
     return QR_OK;
 }
 
+// Host view of the page accounting and SeqLen, read back from the device after
+// device-side appends (a no-op otherwise).
+int sync_host(const qr_mla* cm) {
+    qr_mla* m = const_cast<qr_mla*>(cm);
+    if (!m->store.device_ahead()) return QR_OK;
+    DeviceGuard dg(m->device);
+    std::vector<int> len{m->seq_len};
+    const int st = m->store.pull(len);
+    m->seq_len = len[0];
+    return st;
+}
+
+// Device copy of the accounting after host-side changes (once device-side appends are in use).
+int sync_device(qr_mla* m, hipStream_t stream) {
+    if (!m->device_steps) return QR_OK;
+    return m->store.push(std::vector<int>{m->seq_len}, stream);
+}
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// SeqLen changed on the host (Reset / Truncate): the device copy follows before the call returns.
+int sync_state(qr_mla* m) {
+    if (!m->device_steps) return QR_OK;
+    DeviceGuard dg(m->device);
+    QR_TRY(sync_device(m, m->stream));
+    QR_HIP(hipStreamSynchronize(m->stream));
+    return QR_OK;
+}
+
+// A buffer that may only grow outside stream capture.
+int ensure_outside_capture(DevBuf& b, size_t bytes, hipStream_t stream) {
+    if (bytes <= b.size()) return QR_OK;
+    QR_CHECK_ARG(!capturing(stream), "a buffer must grow to %zu bytes: make one call outside capture first", bytes);
+    return b.ensure(bytes);
+}
+
 int append_dev(qr_mla* m, int layer, int pos0, int n, const void* rows, int len, int src_dtype,
                hipStream_t stream) {
     QR_TRY(m->store.ensure(0, layer, pos0 + n, stream));
@@ -72,11 +113,13 @@ int append_dev(qr_mla* m, int layer, int pos0, int n, const void* rows, int len,
     a.n = n;
     QR_HIP(launch_append(a, stream));
     m->seq_len = std::max(m->seq_len, pos0 + n);  // MlaLatentCache.cs:50
-    return QR_OK;
+    return sync_device(m, stream);
 }
 
-int attention_dev(qr_mla* m, int layer, int pos, int heads, const float* qt, const float* qr_,
-                  float scale, float* u, hipStream_t stream) {
+// pos_dev set: the position is read on the device, pos is ignored and the plan is made
+// for max_seq.
+int attention_dev(qr_mla* m, int layer, int pos, const int* pos_dev, int heads, const float* qt,
+                  const float* qr_, float scale, float* u, hipStream_t stream) {
     MlaArgs a{};
     a.pool = m->store.pool();
     a.page_table = m->store.page_table_dev() + m->store.pt_offset(0, layer);
@@ -84,13 +127,14 @@ int attention_dev(qr_mla* m, int layer, int pos, int heads, const float* qt, con
     a.kv_lora = m->kv_lora;
     a.rope = m->rope;
     a.heads = heads;
-    a.seq_len = pos + 1;
+    a.seq_len = pos_dev ? m->max_seq : pos + 1;
+    a.pos_dev = pos_dev;
     a.q_tilde = qt;
     a.q_rope = qr_;
     a.u = u;
     a.scale = scale;
     const MlaPlan plan = plan_mla(a);
-    QR_TRY(m->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+    QR_TRY(ensure_outside_capture(m->workspace, std::max<size_t>(plan.workspace_bytes, 256), stream));
     QR_HIP(launch_mla(a, plan, m->workspace.get(), stream));
     return QR_OK;
 }
@@ -98,13 +142,13 @@ int attention_dev(qr_mla* m, int layer, int pos, int heads, const float* qt, con
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 // StreamingEngine.cs:508-577 after cache.Append: q-absorb, absorbed attention, W_UV.
-int attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nope, int vdim, const float* q,
-                        const void* kvb, int fmt, float* out, hipStream_t stream) {
+int attend_absorbed_dev(qr_mla* m, int layer, int pos, const int* pos_dev, int heads, int nope, int vdim,
+                        const float* q, const void* kvb, int fmt, float* out, hipStream_t stream) {
     MlaProjArgs a{};
     QR_TRY(mla_proj_prepare(a, kvb, fmt, heads, nope, m->rope, vdim, m->kv_lora));
     const size_t qt_bytes = align256(static_cast<size_t>(heads) * m->kv_lora * 4);
     const size_t qr_bytes = align256(static_cast<size_t>(heads) * std::max(m->rope, 1) * 4);
-    QR_TRY(m->proj.ensure(2 * qt_bytes + qr_bytes));
+    QR_TRY(ensure_outside_capture(m->proj, 2 * qt_bytes + qr_bytes, stream));
     char* base = static_cast<char*>(m->proj.get());
     float* qt = reinterpret_cast<float*>(base);
     float* u = reinterpret_cast<float*>(base + qt_bytes);
@@ -115,7 +159,7 @@ int attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nope, int 
     a.q_rope = m->rope > 0 ? qr_ : nullptr;
     QR_HIP(launch_mla_absorb(a, stream));
     const float scale = 1.0f / std::sqrt(static_cast<float>(nope + m->rope));  // :511
-    QR_TRY(attention_dev(m, layer, pos, heads, qt, qr_, scale, u, stream));
+    QR_TRY(attention_dev(m, layer, pos, pos_dev, heads, qt, qr_, scale, u, stream));
     a.in = u;
     a.out = out;
     a.q_rope = nullptr;
@@ -224,6 +268,7 @@ int qr_mla_destroy(qr_mla* m) {
 int qr_mla_reserve(qr_mla* m, int pages) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     DeviceGuard dg(m->device);
     return m->store.reserve(pages);
 }
@@ -231,6 +276,7 @@ int qr_mla_reserve(qr_mla* m, int pages) {
 int qr_mla_append(qr_mla* m, int layer, int pos, const float* latent, int len) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_TRY(check_layer(m, layer));
     QR_TRY(check_pos(m, pos));
     QR_CHECK_ARG(len >= 0 && (latent || len == 0), "null latent row");
@@ -249,6 +295,7 @@ int qr_mla_append(qr_mla* m, int layer, int pos, const float* latent, int len) {
 int qr_mla_append_range(qr_mla* m, int layer, int pos0, int n, const void* rows, int src_dtype) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_TRY(check_layer(m, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0 && (rows || n == 0), "null rows / negative count");
@@ -268,6 +315,7 @@ int qr_mla_append_range_dev(qr_mla* m, int layer, int pos0, int n, const void* r
                             void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_TRY(check_layer(m, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0 && (rows_dev || n == 0), "null rows / negative count");
@@ -282,6 +330,7 @@ int qr_mla_attention(qr_mla* m, int layer, int pos, int heads, const float* q_ti
                      float scale, float* u) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(q_tilde && u && (q_rope || m->rope == 0), "null q_tilde/q_rope/u pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     DeviceGuard dg(m->device);
@@ -294,7 +343,7 @@ int qr_mla_attention(qr_mla* m, int layer, int pos, int heads, const float* q_ti
     float* dqr = reinterpret_cast<float*>(st + 2 * qt_bytes);
     QR_HIP(hipMemcpyAsync(dqt, q_tilde, qt_bytes, hipMemcpyHostToDevice, m->stream));
     if (qr_bytes) QR_HIP(hipMemcpyAsync(dqr, q_rope, qr_bytes, hipMemcpyHostToDevice, m->stream));
-    QR_TRY(attention_dev(m, layer, pos, heads, dqt, dqr, scale, du, m->stream));
+    QR_TRY(attention_dev(m, layer, pos, nullptr, heads, dqt, dqr, scale, du, m->stream));
     QR_HIP(hipMemcpyAsync(u, du, qt_bytes, hipMemcpyDeviceToHost, m->stream));
     QR_HIP(hipStreamSynchronize(m->stream));
     return QR_OK;
@@ -304,10 +353,11 @@ int qr_mla_attention_dev(qr_mla* m, int layer, int pos, int heads, const float* 
                          const float* q_rope_dev, float scale, float* u_dev, void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(q_tilde_dev && u_dev && (q_rope_dev || m->rope == 0), "null q_tilde/q_rope/u pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     DeviceGuard dg(m->device);
-    return attention_dev(m, layer, pos, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
+    return attention_dev(m, layer, pos, nullptr, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
                          static_cast<hipStream_t>(stream));
 }
 
@@ -315,6 +365,7 @@ int qr_mla_attend_absorbed(qr_mla* m, int layer, int pos, int heads, int nope, i
                            const qr_weight* kvb, float* out) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(q && out && kvb, "null q / kvb / out pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     QR_CHECK_ARG(nope >= 1 && vdim >= 1, "bad nope %d / vdim %d", nope, vdim);
@@ -330,7 +381,7 @@ int qr_mla_attend_absorbed(qr_mla* m, int layer, int pos, int heads, int nope, i
     float* dq = reinterpret_cast<float*>(st);
     float* dout = reinterpret_cast<float*>(st + align256(q_bytes));
     QR_HIP(hipMemcpyAsync(dq, q, q_bytes, hipMemcpyHostToDevice, m->stream));
-    QR_TRY(attend_absorbed_dev(m, layer, pos, heads, nope, vdim, dq, kvb->dev, kvb->format, dout, m->stream));
+    QR_TRY(attend_absorbed_dev(m, layer, pos, nullptr, heads, nope, vdim, dq, kvb->dev, kvb->format, dout, m->stream));
     QR_HIP(hipMemcpyAsync(out, dout, o_bytes, hipMemcpyDeviceToHost, m->stream));
     QR_HIP(hipStreamSynchronize(m->stream));
     return QR_OK;
@@ -340,30 +391,34 @@ int qr_mla_attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nop
                                const void* kvb_dev, int kvb_format, float* out_dev, void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(q_dev && out_dev, "null q / out pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     DeviceGuard dg(m->device);
-    return attend_absorbed_dev(m, layer, pos, heads, nope, vdim, q_dev, kvb_dev, kvb_format, out_dev,
+    return attend_absorbed_dev(m, layer, pos, nullptr, heads, nope, vdim, q_dev, kvb_dev, kvb_format, out_dev,
                                static_cast<hipStream_t>(stream));
 }
 
 int qr_mla_reset(qr_mla* m) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     m->seq_len = 0;
-    return QR_OK;
+    return sync_state(m);
 }
 
 int qr_mla_truncate(qr_mla* m, int len) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     if (len < m->seq_len) m->seq_len = len;  // MlaLatentCache.cs:57
-    return QR_OK;
+    return sync_state(m);
 }
 
 int qr_mla_seq_len(const qr_mla* m, int* out) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(out, "null output pointer");
     *out = m->seq_len;
     return QR_OK;
@@ -372,6 +427,7 @@ int qr_mla_seq_len(const qr_mla* m, int* out) {
 int qr_mla_bytes_used(const qr_mla* m, long long* out) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_CHECK_ARG(out, "null output pointer");
     *out = m->store.bytes_used();
     return QR_OK;
@@ -380,6 +436,7 @@ int qr_mla_bytes_used(const qr_mla* m, long long* out) {
 int qr_mla_page_count(const qr_mla* m, int layer, int* out) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_TRY(check_layer(m, layer));
     QR_CHECK_ARG(out, "null output pointer");
     *out = m->store.pages_held(0, layer);
@@ -389,6 +446,7 @@ int qr_mla_page_count(const qr_mla* m, int layer, int* out) {
 int qr_mla_read_page(qr_mla* m, int layer, int page, float* out) {
     clear_error();
     QR_TRY(check_handle(m));
+    QR_TRY(sync_host(m));
     QR_TRY(check_layer(m, layer));
     QR_CHECK_ARG(out, "null output pointer");
     QR_CHECK_ARG(page >= 0 && page < m->store.pages_held(0, layer), "page %d outside [0, %d)", page,
@@ -409,6 +467,86 @@ int qr_mla_read_page(qr_mla* m, int layer, int page, float* out) {
     QR_HIP(hipMemcpyAsync(out, m->stage.get(), bytes, hipMemcpyDeviceToHost, m->stream));
     QR_HIP(hipStreamSynchronize(m->stream));
     return QR_OK;
+}
+
+int qr_mla_append_step_dev(qr_mla* m, int layer, int n, const int* pos0_dev, const void* rows_dev, int src_dtype,
+                           void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
+    QR_CHECK_ARG(pos0_dev && rows_dev, "null pos/rows pointer");
+    QR_CHECK_ARG(n >= 1 && n <= m->max_seq, "n %d outside [1, %d]", n, m->max_seq);
+    DeviceGuard dg(m->device);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool cap = capturing(st);
+    if (!m->device_steps) {
+        // first device-side append: the device copy starts from the host accounting
+        QR_CHECK_ARG(!cap, "the first device-side append of a cache must run outside stream capture");
+        QR_TRY(sync_host(m));
+        m->device_steps = true;
+        QR_TRY(m->store.push(std::vector<int>{m->seq_len}, st));
+    }
+    if (m->store.capacity() < 1) {
+        QR_CHECK_ARG(!cap, "the page pool is empty: reserve pages before capturing device-side appends");
+        QR_TRY(m->store.reserve(16));
+    }
+    PageClaimArgs c{};
+    c.page_table = const_cast<int*>(m->store.page_table_dev()) + m->store.pt_offset(0, layer);
+    c.state = m->store.state_dev();
+    c.held_index = m->store.held_index(0, layer);
+    c.seq_index = m->store.seq_index(0);
+    c.capacity = static_cast<int>(std::min<long long>(m->store.capacity(), 0x7FFFFFFF));
+    c.max_seq = m->max_seq;
+    c.pos_dev = pos0_dev;
+    c.n = n;
+    QR_HIP(launch_page_claim(c, st));
+    AppendArgs a{};
+    a.pool = m->store.pool();
+    a.page_table = m->store.page_table_dev() + m->store.pt_offset(0, layer);
+    a.geom = m->store.geom();
+    a.dtype = m->dtype;
+    a.src[0] = rows_dev;
+    a.row_len[0] = m->latent;
+    a.src_stride = m->latent;
+    a.src_dtype = src_dtype;
+    a.pos0 = 0;
+    a.n = n;
+    a.pos_dev = pos0_dev;
+    a.held_dev = m->store.state_dev() + c.held_index;
+    a.max_seq = m->max_seq;
+    QR_HIP(launch_append(a, st));
+    m->store.mark_device_ahead();
+    return QR_OK;
+}
+
+int qr_mla_attention_step_dev(qr_mla* m, int layer, const int* pos_dev, int heads, const float* q_tilde_dev,
+                              const float* q_rope_dev, float scale, float* u_dev, void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(pos_dev && q_tilde_dev && u_dev && (q_rope_dev || m->rope == 0), "null pos/q_tilde/q_rope/u pointer");
+    QR_CHECK_ARG(m->split_set, "the latent's kv_lora/rope split is not set (qr_mla_set_rope)");
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(heads >= 1 && heads <= kMlaMaxHeads, "heads %d outside [1, %d]", heads, kMlaMaxHeads);
+    QR_CHECK_ARG(m->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
+    DeviceGuard dg(m->device);
+    return attention_dev(m, layer, 0, pos_dev, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
+                         static_cast<hipStream_t>(stream));
+}
+
+int qr_mla_attend_absorbed_step_dev(qr_mla* m, int layer, const int* pos_dev, int heads, int nope, int vdim,
+                                    const float* q_dev, const void* kvb_dev, int kvb_format, float* out_dev,
+                                    void* stream) {
+    clear_error();
+    QR_TRY(check_handle(m));
+    QR_CHECK_ARG(pos_dev && q_dev && out_dev, "null pos / q / out pointer");
+    QR_CHECK_ARG(m->split_set, "the latent's kv_lora/rope split is not set (qr_mla_set_rope)");
+    QR_TRY(check_layer(m, layer));
+    QR_CHECK_ARG(heads >= 1 && heads <= kMlaMaxHeads, "heads %d outside [1, %d]", heads, kMlaMaxHeads);
+    QR_CHECK_ARG(m->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
+    DeviceGuard dg(m->device);
+    return attend_absorbed_dev(m, layer, 0, pos_dev, heads, nope, vdim, q_dev, kvb_dev, kvb_format, out_dev,
+                               static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

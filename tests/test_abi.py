@@ -80,6 +80,10 @@ def test_null_handles_are_rejected():
         _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_attention_chunk_step_dev(None, 0, 0, 4, None, None, 0, None, 1.0, None) == \
         _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_append_step_dev(None, 0, 1, None, None, 0, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_attention_step_dev(None, 0, None, 8, None, None, 1.0, None, None) == _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_mla_attend_absorbed_step_dev(None, 0, None, 8, 128, 128, None, None, 1, None, None) == \
+        _lib.QR_ERR_INVALID_ARGUMENT
     assert L.qr_kv_destroy(None) == 0 and L.qr_mla_destroy(None) == 0
     assert "null" in L.qr_last_error().decode() or L.qr_last_error() == b""
 

@@ -19,7 +19,7 @@ import pytest
 
 import qauntrunner_amd as qr
 from qauntrunner_amd._lib import QrOutOfMemory, QrOutOfRange
-from tests.util import normal
+from tests.util import errors, normal
 
 pytestmark = pytest.mark.gpu
 
@@ -315,3 +315,111 @@ def test_captured_chunk_step_replays_at_advancing_positions(gpu, dtype):
             ka, va = A.Read(layer, 0, end)
             kb, vb = B.Read(layer, 0, end)
             assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}"
+
+
+@pytest.mark.parametrize("dtype,heads,rope,max_seq", [("bf16", 32, 64, 4096), ("bf16", 32, 64, 65536),
+                                                      ("f32", 8, 64, 4096)])
+def test_mla_steps_match_the_host_path(gpu, dtype, heads, rope, max_seq):
+    """qr_mla_append_step_dev + qr_mla_attention_step_dev against the host-position calls:
+    16-bit latents take the MFMA tile kernel (the sequence spreads over the splits planned for
+    max_seq), fp32 latents the generic kernel; single-row and multi-row appends."""
+    import torch
+
+    kv_lora = 512
+    W = kv_lora + rope
+    p0 = 250
+    rows = normal(1200, (p0 + 40, W)).astype(np.float32)
+    qt, qr_ = normal(1201, (heads, kv_lora)), normal(1202, (heads, rope))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1 / np.sqrt(192)
+    with qr.MlaLatentCache(1, W, max_seq, dtype=dtype, rope=rope) as A, \
+            qr.MlaLatentCache(1, W, max_seq, dtype=dtype, rope=rope) as B:
+        for m in (A, B):
+            m.AppendRangeDev(0, 0, dev(rows[:p0]))
+        pos = torch.zeros(1, dtype=torch.int32, device=gpu)
+        t = p0
+        for n in (1, 1, 5, 1, 12):  # crosses the page boundary at 256
+            A.AppendRangeDev(0, t, dev(rows[t:t + n]))
+            pos.fill_(t)
+            B.AppendStepDev(0, pos, dev(rows[t:t + n]))
+            t += n
+            ua, ub = torch.empty(heads, kv_lora, device=gpu), torch.empty(heads, kv_lora, device=gpu)
+            A.AbsorbedAttentionDev(0, t - 1, dev(qt), dev(qr_), ua, scale)
+            pos.fill_(t - 1)
+            B.AbsorbedAttentionStepDev(0, pos, dev(qt), dev(qr_), ub, scale)
+            torch.cuda.synchronize()
+            want, got = ua.cpu().numpy(), ub.cpu().numpy()
+            a, r = errors(got, want)
+            assert r <= (1e-6 if dtype == "f32" else 1e-3), f"attention at {t - 1}: rel {r:.2e}"
+        assert B.SeqLen == A.SeqLen == t
+        assert B.BytesUsed == A.BytesUsed and B.PageCount(0) == A.PageCount(0)
+        for pg in range(A.PageCount(0)):
+            assert np.array_equal(A.Page(0, pg), B.Page(0, pg)), f"page {pg}"
+        B.Truncate(100)
+        pos.fill_(100)
+        B.AppendStepDev(0, pos, dev(rows[:1]))
+        assert B.SeqLen == 101
+
+
+def test_captured_mla_layer_step_replays_at_advancing_positions(gpu):
+    """Append + absorbed layer block (q-absorb, attention, W_UV) at a device position,
+    captured once and replayed at 20 advancing positions across a page boundary."""
+    import torch
+
+    heads, nope, rope, vdim, kv_lora, max_seq = 32, 128, 64, 128, 512, 8192
+    W = kv_lora + rope
+    p0, steps = 500, 20
+    rows = normal(1300, (p0 + steps + 1, W)).astype(np.float32)
+    kvb = normal(1301, (heads * (nope + vdim), kv_lora)).astype(np.float32) * 0.05
+    qs = normal(1302, (p0 + steps + 1, heads * (nope + rope)))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    with qr.MlaLatentCache(1, W, max_seq, dtype="bf16", rope=rope) as A, \
+            qr.MlaLatentCache(1, W, max_seq, dtype="bf16", rope=rope) as B:
+        Wt = qr.Weight("F32", heads * (nope + vdim), kv_lora, kvb.view(np.uint8))
+        for m in (A, B):
+            m.AppendRangeDev(0, 0, dev(rows[:p0]))
+        B.Reserve(16)
+        pos = torch.zeros(1, dtype=torch.int32, device=gpu)
+        row_buf = torch.empty(1, W, device=gpu)
+        q_buf = torch.empty(heads, nope + rope, device=gpu)
+        out_b = torch.empty(heads, vdim, device=gpu)
+
+        def step_b():
+            B.AppendStepDev(0, pos, row_buf)
+            B.AttendAbsorbedStepDev(0, pos, q_buf, Wt, Wt.Fmt, nope, vdim, out_b)
+
+        def load(t):
+            pos.fill_(t)
+            row_buf.copy_(dev(rows[t:t + 1]))
+            q_buf.copy_(dev(qs[t].reshape(heads, nope + rope)))
+
+        def check(t):
+            A.AppendRangeDev(0, t, dev(rows[t:t + 1]))
+            out_a = torch.empty(heads, vdim, device=gpu)
+            A.AttendAbsorbedDev(0, t, dev(qs[t].reshape(heads, nope + rope)), Wt, Wt.Fmt, nope, vdim, out_a)
+            torch.cuda.synchronize()
+            a, r = errors(out_b.cpu().numpy(), out_a.cpu().numpy())
+            assert r <= 1e-3, f"layer block at {t}: rel {r:.2e}"
+
+        load(p0)
+        step_b()  # eager first call: device accounting, workspaces
+        torch.cuda.synchronize()
+        check(p0)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            load(p0 + 1)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step_b()
+        for t in range(p0 + 1, p0 + steps + 1):
+            load(t)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            check(t)
+        assert B.SeqLen == A.SeqLen == p0 + steps + 1
+        for pg in range(A.PageCount(0)):
+            assert np.array_equal(A.Page(0, pg), B.Page(0, pg)), f"page {pg}"
+        Wt.close()
