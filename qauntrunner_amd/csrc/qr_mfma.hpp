@@ -50,6 +50,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
+constexpr int kCacheSc1 = 16;             // buffer intrinsic cache-policy bits: sc1 (device scope)
 
 // 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
 // ... lds); out-of-range offsets read zeros.  `lds` must be the same for every lane of
