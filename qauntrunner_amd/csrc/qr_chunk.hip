@@ -128,9 +128,11 @@ __global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const 
     // keeps that kv head's K/V (4 MB at 8192 positions, head_dim 128) instead of every
     // L2 cycling through all kv heads.  The first half of a kv head's run takes its query
     // blocks from the last (most keys under the causal mask) down, the second half from
-    // the first up: with two workgroups per CU, the XCD's k-th and (k + 32)-th workgroups
-    // tend to share a CU and then sum to about the same keys (measured at 2048 queries
-    // after 6144 positions: 255 us per call against 263 with all blocks descending).
+    // the first up: with two workgroups per CU resident at once, launch slots b and
+    // b + 256 run on one CU (the XCD's k-th and (k + 32)-th workgroups; measured with a
+    // probe of the hardware CU ids, the same on every launch), so the pair sums to about
+    // the same keys (2048 queries after 6144 positions: 255 us per call against 263 with
+    // all blocks descending).
     const int bslot = blockIdx.x;
     const int unit = (bslot & 7) * p.per_xcd + (bslot >> 3);
     if (unit >= p.units) return;
