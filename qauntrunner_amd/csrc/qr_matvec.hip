@@ -559,7 +559,10 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
 // registers.  A tile is R rows (R * row_bytes <= 4 KiB * U); wave w loads its 1 KiB units
 // w, w + 4, ... of it.  Per tile: wait for this wave's units, barrier (every wave's units have
 // landed and the slot refilled next has been read), refill, compute the tile's terms from LDS.
-constexpr int kRingSlots = 3;  // deeper rings measured slower: fewer workgroups fit per CU
+// Two slots: one tile in flight while one is read, and more workgroups per CU (measured
+// per 8B layer of Q8_0 MatVecs: 82.9 us, against 87.4-88.8 with three slots; deeper rings
+// slower still)
+constexpr int kRingSlots = 2;
 
 struct MvRing {
     int P, tpg, rg, R, tstride;
@@ -653,7 +656,11 @@ __global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
 // ring of kFwSlots LDS slots filled by direct-to-LDS buffer loads (kFwSlots - 1 segments in
 // flight; completion awaited with explicit vmcnt waits), and each lane walks its chain over
 // the chunks of a segment: weight, x, product, add.  No barrier, no register prefetch.
-constexpr int kFwSlots = 3;
+// Two slots (one segment in flight while one is read): 20.6 KiB of LDS per one-wave
+// workgroup, so 7 fit per CU and the 14336-row matrices of the 8B shape (1,792 workgroups)
+// run in one round.  Measured per 8B layer of F16 MatVecs: 113.0 us, against 116.6-118.3
+// with three slots and 125.9-127.0 with four.
+constexpr int kFwSlots = 2;
 constexpr int kFwRowPad = 1024 + 16;  // LDS bytes per row segment: rows land on distinct banks
 
 template <int FMT, int R>
