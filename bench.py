@@ -69,7 +69,8 @@ WORKLOADS = {
                             desc="MLA absorbed layer block as f2-mla-layer with the kvb weights in Q8_0"),
     "f3-matvec-q4k": dict(kind="matvec", wfmt="Q4_K", dtype="f32", B=1,
                           desc="fused dequant + dot MatVecs of one llama-3-8b layer for one token: wq, wk, wv, wo "
-                               "(4096/1024 x 4096), gate, up (14336 x 4096), down (4096 x 14336), Q4_K weights"),
+                               "(4096/1024 x 4096), gate, up (14336 x 4096), down (4096 x 14336), Q4_K weights; "
+                               "wq/wk/wv and gate/up as grouped calls on their shared input"),
     "f3-matvec-q8": dict(kind="matvec", wfmt="Q8_0", dtype="f32", B=1,
                          desc="the f3-matvec-q4k projections with Q8_0 weights"),
     "f3-matvec-f16": dict(kind="matvec", wfmt="F16", dtype="f32", B=1,
@@ -77,7 +78,7 @@ WORKLOADS = {
     "f4-stream-q4k": dict(kind="stream", wfmt="Q4_K", layers=8, budget=160 << 20, dtype="f32", B=1,
                           desc="weight streaming: 8 llama-3-8b-shape Q4_K layers (wq, wk, wv, wo, gate, up, down "
                                "and two norms) read from a .qw file in the page cache through the two HBM "
-                               "prefetch slots, each layer's 7 MatVecs for one token queued behind its upload"),
+                               "prefetch slots, each layer's 7 MatVecs for one token (4 grouped calls) queued behind its upload"),
 }
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
@@ -87,9 +88,16 @@ MATVEC_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336,
 W_FORMATS = {"F16": (1, 1, 2), "Q8_0": (4, 32, 34), "Q4_K": (6, 256, 144)}  # code, block, bytes
 
 
+# projections that read one activation vector run as one grouped call (qr_matvec_group_dev):
+# wq/wk/wv of the normed x and gate/up of the normed FFN input (StreamingEngine.cs:240-242,
+# :605-606); wo and down alone
+MATVEC_GROUPS = [[0, 1, 2], [3], [4, 5], [6]]
+
+
 def matvec_bytes(w):
     code, bs, bb = W_FORMATS[w["wfmt"]]
-    return sum(r * (c // bs) * bb + c * 4 + r * 4 for r, c in MATVEC_SHAPES)
+    weights = sum(r * (c // bs) * bb + r * 4 for r, c in MATVEC_SHAPES)
+    return weights + sum(MATVEC_SHAPES[g[0]][1] * 4 for g in MATVEC_GROUPS)  # x once per group
 
 
 STREAM_NAMES = ["wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"]  # MATVEC_SHAPES order
@@ -352,12 +360,20 @@ def run_gpu(w, steps, warmup):
         xs = [torch.randn(c, device=dev, generator=gen) for _, c in MATVEC_SHAPES]
         ys = [torch.empty(r, device=dev) for r, _ in MATVEC_SHAPES]
 
-        for k, (r, c) in enumerate(MATVEC_SHAPES):
-            qr.matvec_dev(mats[0][k], code, r, c, xs[k], ys[k], stream=stream)
+        for g in MATVEC_GROUPS:
+            qr.matvec_group_dev([mats[0][k] for k in g], code, [MATVEC_SHAPES[k][0] for k in g],
+                                MATVEC_SHAPES[g[0]][1], xs[g[0]], [ys[k] for k in g], stream=stream)
         lib = qr.load()
         sp = ctypes.c_void_p(stream.cuda_stream)
-        calls = [[prepared(lib.qr_matvec_dev, m[k].data_ptr(), code, ctypes.c_longlong(r), c, 1, xs[k].data_ptr(),
-                           ys[k].data_ptr(), sp) for k, (r, c) in enumerate(MATVEC_SHAPES)] for m in mats]
+
+        def group_call(m, g):
+            n = len(g)
+            wp = (ctypes.c_void_p * n)(*[m[k].data_ptr() for k in g])
+            rp = (ctypes.c_longlong * n)(*[MATVEC_SHAPES[k][0] for k in g])
+            yp = (ctypes.c_void_p * n)(*[ys[k].data_ptr() for k in g])
+            return prepared(lib.qr_matvec_group_dev, n, wp, rp, code, MATVEC_SHAPES[g[0]][1], 1, xs[g[0]].data_ptr(),
+                            yp, sp)
+        calls = [[group_call(m, g) for g in MATVEC_GROUPS] for m in mats]
 
         def step(i):
             for call in calls[i % R]:
@@ -382,9 +398,10 @@ def run_gpu(w, steps, warmup):
             """StreamingEngine.Forward's weight order (StreamingEngine.cs:225-266)."""
             p.Begin(0)
             for l in range(L):
-                for k, (r, c) in enumerate(MATVEC_SHAPES):
-                    wt = p.Acquire(f"l{l}.{STREAM_NAMES[k]}", l, stream)
-                    qr.matvec_dev(wt, code, r, c, xs[k], ys[k], stream=stream)
+                wts = [p.Acquire(f"l{l}.{STREAM_NAMES[k]}", l, stream) for k in range(len(MATVEC_SHAPES))]
+                for g in MATVEC_GROUPS:
+                    qr.matvec_group_dev([wts[k] for k in g], code, [MATVEC_SHAPES[k][0] for k in g],
+                                        MATVEC_SHAPES[g[0]][1], xs[g[0]], [ys[k] for k in g], stream=stream)
                 p.Release(l, stream)
                 if l + 1 < L:
                     p.Begin(l + 1)
@@ -870,7 +887,8 @@ def main():
     if kernel_ms:
         roof["split_kernel_us"] = round(kernel_ms * 1e3, 3)
     if w["kind"] == "stream":
-        roof["kernel"] = f"the {7 * w['layers']} MatVecs of a resident forward (HIP events)"
+        roof["kernel"] = (f"the {7 * w['layers']} MatVecs ({len(MATVEC_GROUPS) * w['layers']} grouped launches) of a "
+                          "resident forward (HIP events)")
     line = {
         "metric": METRIC,
         "value": round(tbs, 4),

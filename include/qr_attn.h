@@ -339,6 +339,15 @@ int qr_mla_wuv_dev(const void* kvb_dev, int kvb_format, int heads, int nope, int
  * and a multiple of 8 for F32/F16/BF16. */
 int qr_matvec_dev(const void* w_dev, int format, long long rows, int cols, int nq, const float* x_dev,
                   float* y_dev, void* stream);
+/* n <= 4 MatVecs that read the same x -- the projections of one activation vector, as
+ * StreamingEngine.cs:240-242 (wq, wk, wv of the normed x) and :605-606 (gate and up) call
+ * MatVecParallel on them one after another -- with one launch for F32/F16/BF16 rows (the
+ * other formats run one launch per matrix).  Same format and cols for every matrix; matrix m
+ * has rows[m] rows at w_devs[m] (16-byte aligned) and writes y_devs[m] [nq][rows[m]].  Every
+ * y equals qr_matvec_dev's for that matrix, bit for bit.  No counterpart in the reference:
+ * for callers that run a layer's projections on the GPU. */
+int qr_matvec_group_dev(int n, const void* const* w_devs, const long long* rows, int format, int cols, int nq,
+                        const float* x_dev, float* const* y_devs, void* stream);
 /* Same with host vectors against an uploaded weight (synchronous; not thread-safe per weight). */
 int qr_matvec(const qr_weight* w, int nq, const float* x, float* y);
 

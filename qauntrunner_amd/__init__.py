@@ -21,12 +21,12 @@ from ._lib import (
 )
 from .caches import MlaLatentCache, PagedKvCache, dtype_code
 from .store import DeviceTensor, ModelStore, ModelStoreBuilder, PrefetchPipeline, TensorView
-from .weights import Weight, matvec_dev, mla_q_absorb_dev, mla_wuv_dev
+from .weights import Weight, matvec_dev, matvec_group_dev, mla_q_absorb_dev, mla_wuv_dev
 
 __all__ = [
     "DTYPE_BF16", "DTYPE_F16", "DTYPE_F32", "LIB_PATH", "PAGE_TOKENS",
     "QrError", "QrHipError", "QrInvalidArgument", "QrNotResident", "QrOutOfMemory", "QrOutOfRange",
     "load", "MlaLatentCache", "PagedKvCache", "dtype_code",
-    "Weight", "matvec_dev", "mla_q_absorb_dev", "mla_wuv_dev",
+    "Weight", "matvec_dev", "matvec_group_dev", "mla_q_absorb_dev", "mla_wuv_dev",
     "DeviceTensor", "ModelStore", "ModelStoreBuilder", "PrefetchPipeline", "TensorView",
 ]

@@ -124,6 +124,7 @@ SIGNATURES = {
     "qr_mla_q_absorb_dev": [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     "qr_mla_wuv_dev": [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p],
     "qr_matvec_dev": [_p, _i, ctypes.c_longlong, _i, _i, _p, _p, _p],
+    "qr_matvec_group_dev": [_i, _p, _p, _i, _i, _i, _p, _p, _p],
     "qr_matvec": [_p, _i, _p, _p],
     "qr_model_open": [_pp, ctypes.c_char_p],
     "qr_model_close": [_p],

@@ -318,7 +318,7 @@ __device__ __forceinline__ void q4k_pair_terms(const u32x4_t h, const u32x4_t qa
 }
 
 // Persistent form of the block formats: workgroup w takes row tiles w, w + G, w + 2G, ...
-// (G = gridDim.x, R rows a tile).  Thread (row group g, item column pc) owns one item of every
+// (G = the workgroups of its matrix, R rows a tile).  Thread (row group g, item column pc) owns one item of every
 // row (Q4_K: a sub-block pair, 64 columns, two terms; Q8_0: a block pair, 64 columns, two
 // terms): its x values stay in registers for all tiles, the next tile's weights are loaded
 // while the current tile is computed (two register buffers, the loop unrolled by two so that
@@ -365,6 +365,26 @@ struct MvBlkP {
     int P, tpg, rg, R, tstride;
     int ntiles;   // ceil(rows / R)
 };
+
+// Matrices of one launch of the block kernels: workgroups start[m] .. start[m + 1] - 1 take
+// matrix m (its own tiles, strided by its workgroup count), every matrix sharing the
+// format, cols and x (a single MatVec is a group of one).
+struct BlkGroup {
+    int n;
+    int start[kMatVecGroupMax + 1];
+    int ntiles[kMatVecGroupMax];
+    const uint8_t* w[kMatVecGroupMax];
+    long long rows[kMatVecGroupMax];
+    float* y[kMatVecGroupMax];
+};
+
+__device__ __forceinline__ int group_member(int n, const int (&start)[kMatVecGroupMax + 1]) {
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < kMatVecGroupMax; ++i)
+        if (i < n && static_cast<int>(blockIdx.x) >= start[i]) m = i;
+    return m;
+}
 
 // Q4_K (DotKernels.cs:322-373): item pc = 4*block + j; loads: the block header and the two
 // 16-byte quant vectors of pair j.
@@ -481,17 +501,23 @@ __device__ __forceinline__ void blk_load(const MatVecArgs& a, const MvBlkP& k, i
 }
 
 template <class Pol, int RPT>
-__global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlkP k) {
+__global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlkP k, BlkGroup gr) {
     typedef typename PolLoad<Pol>::type V;
     extern __shared__ __align__(16) uint8_t mv_lds[];
     float* terms = reinterpret_cast<float*>(mv_lds);
+    const int mg = group_member(gr.n, gr.start);  // this workgroup's matrix (uniform)
+    a.w = gr.w[mg];
+    a.rows = gr.rows[mg];
+    a.y = gr.y[mg];
+    k.ntiles = gr.ntiles[mg];
+    const int bx = static_cast<int>(blockIdx.x) - gr.start[mg];
     const int t = threadIdx.x;
     const int g = t / k.tpg;
     const bool active = t - g * k.tpg < k.P;
     // lanes past the row's items load and compute item P-1 and store nothing: no branch
     // around the loads, so the wait counts stay exact
     const int pc = min(t - g * k.tpg, k.P - 1);
-    const int G = gridDim.x;
+    const int G = gr.start[mg + 1] - gr.start[mg];
     const int q = blockIdx.y;
     const float* x = a.x + static_cast<long long>(q) * a.cols;
     const int last = k.ntiles - 1;
@@ -506,7 +532,7 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
             for (int i = 0; i < Pol::kLoads; ++i) off[r][i] = static_cast<uint32_t>((g * RPT + r) * a.row_bytes) + o[i];
     }
     V vA[RPT][Pol::kLoads], vB[RPT][Pol::kLoads];
-    int it = blockIdx.x;
+    int it = bx;
     blk_load<Pol, RPT>(a, k, it, off, vA);
     // x reaches the threads through LDS: one coalesced copy per workgroup (every thread of
     // every workgroup reading its 64 values from global memory made all CUs hit the same
@@ -547,7 +573,7 @@ __global__ __launch_bounds__(512) void matvec_blk_persistent(MatVecArgs a, MvBlk
     const int nt = 2 * k.P;
     for (int i = t; i < slot * k.R; i += blockDim.x) {
         const int s = i / k.R, r = i - s * k.R;
-        const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
+        const long long row = static_cast<long long>(bx + s * G) * k.R + r;
         if (row >= a.rows) continue;
         a.y[static_cast<long long>(q) * a.rows + row] = ordered_row_sum(terms + i * k.tstride, nt);
     }
@@ -587,26 +613,32 @@ __device__ __forceinline__ void ring_read(const char* tile, int row_bytes, int g
 }
 
 template <class Pol, int RPT, int U>
-__global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
+__global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k, BlkGroup gr) {
     typedef typename PolLoad<Pol>::type V;
     extern __shared__ __align__(1024) char ring_lds[];
     float* terms = reinterpret_cast<float*>(ring_lds + kRingSlots * k.slot_bytes);
+    const int mg = group_member(gr.n, gr.start);  // this workgroup's matrix (uniform)
+    a.w = gr.w[mg];
+    a.rows = gr.rows[mg];
+    a.y = gr.y[mg];
+    k.ntiles = gr.ntiles[mg];
+    const int bx = static_cast<int>(blockIdx.x) - gr.start[mg];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // four waves
     const int g = t / k.tpg;
     const bool active = t - g * k.tpg < k.P;
     const int pc = min(t - g * k.tpg, k.P - 1);
-    const int G = gridDim.x;
+    const int G = gr.start[mg + 1] - gr.start[mg];
     const int q = blockIdx.y;
     const float* x = a.x + static_cast<long long>(q) * a.cols;
-    const int cnt = (k.ntiles - static_cast<int>(blockIdx.x) + G - 1) / G;  // tiles of this workgroup, >= 1
+    const int cnt = (k.ntiles - bx + G - 1) / G;  // tiles of this workgroup, >= 1
 
     // DMA of the workgroup's tile s (clamped to its last one, so every round issues U units
     // per wave) into ring slot s % kRingSlots; rows past the matrix read as zero
     auto dma = [&](int s) {
         s = min(s, cnt - 1);
-        const int r0 = (static_cast<int>(blockIdx.x) + s * G) * k.R;
+        const int r0 = (bx + s * G) * k.R;
         const int nrec = min(k.R, static_cast<int>(a.rows) - r0) * static_cast<int>(a.row_bytes);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t*>(a.w + static_cast<long long>(r0) * a.row_bytes), static_cast<short>(0), nrec,
@@ -644,7 +676,7 @@ __global__ __launch_bounds__(256) void matvec_blk_ring(MatVecArgs a, MvRing k) {
     const int nt = 2 * k.P;
     for (int i = t; i < cnt * k.R; i += blockDim.x) {
         const int s = i / k.R, r = i - s * k.R;
-        const long long row = static_cast<long long>(blockIdx.x + s * G) * k.R + r;
+        const long long row = static_cast<long long>(bx + s * G) * k.R + r;
         if (row >= a.rows) continue;
         a.y[static_cast<long long>(q) * a.rows + row] = ordered_row_sum(terms + i * k.tstride, nt);
     }
@@ -685,13 +717,30 @@ __device__ __forceinline__ float fw_product(const char* p, float x) {
     else return __builtin_fmaf(static_cast<float>(*reinterpret_cast<const _Float16*>(p)), x, 0.0f);
 }
 
+// Matrices of one launch: workgroups start[m] .. start[m + 1] - 1 take matrix m (a single
+// MatVec is a group of one).  Every matrix shares the format, cols, row bytes and x.
+struct FwGroup {
+    int n;
+    int start[kMatVecGroupMax + 1];
+    const uint8_t* w[kMatVecGroupMax];
+    long long rows[kMatVecGroupMax];
+    float* y[kMatVecGroupMax];
+};
+
 template <int FMT, int R>
-__global__ __launch_bounds__(64) void matvec_fp_wave(MatVecArgs a) {
+__global__ __launch_bounds__(64) void matvec_fp_wave(MatVecArgs a, FwGroup gr) {
     using Gm = FwGeom<FMT, R>;
     __shared__ __align__(16) char ring[kFwSlots][Gm::SLOT];
     const int lane = threadIdx.x;
     const int rr = lane >> 3, L = lane & 7;
-    const long long r0 = static_cast<long long>(blockIdx.x) * R;
+    int mg = 0;  // this workgroup's matrix (uniform)
+#pragma unroll
+    for (int i = 1; i < kMatVecGroupMax; ++i)
+        if (i < gr.n && static_cast<int>(blockIdx.x) >= gr.start[i]) mg = i;
+    a.w = gr.w[mg];
+    a.rows = gr.rows[mg];
+    a.y = gr.y[mg];
+    const long long r0 = static_cast<long long>(static_cast<int>(blockIdx.x) - gr.start[mg]) * R;
     const int q = blockIdx.y;
     const float* x = a.x + static_cast<long long>(q) * a.cols;
     const int nch = a.cols / 8;
@@ -1137,7 +1186,8 @@ constexpr int kBlkRptQ4k = 2;  // Q4_K rows per thread and tile (Q8_0: 1, its 17
 constexpr int kBlkWgPerCu = 2;  // workgroups of 256 threads per CU (measured: 1 and 3 slower for Q4_K)
 
 template <int U>
-hipError_t ring_launch_q8(const MatVecArgs& a, const MvRing& k, dim3 grid, size_t lds, hipStream_t stream) {
+hipError_t ring_launch_q8(const MatVecArgs& a, const MvRing& k, const BlkGroup& gr, dim3 grid, size_t lds,
+                          hipStream_t stream) {
     static bool attr = false;  // dynamic LDS above 64 KiB must be allowed per kernel
     if (lds > 64 * 1024 && !attr) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_blk_ring<PolQ8, 1, U>),
@@ -1145,48 +1195,91 @@ hipError_t ring_launch_q8(const MatVecArgs& a, const MvRing& k, dim3 grid, size_
         if (e != hipSuccess) return e;
         attr = true;
     }
-    hipLaunchKernelGGL((matvec_blk_ring<PolQ8, 1, U>), grid, dim3(kMvThreads), lds, stream, a, k);
+    hipLaunchKernelGGL((matvec_blk_ring<PolQ8, 1, U>), grid, dim3(kMvThreads), lds, stream, a, k, gr);
     return hipGetLastError();
 }
 
 // The ring form, used for Q8_0 (Q4_K is VALU-bound and measures faster in the persistent
 // form): block pairs, rows of at most 256 pairs (16384 columns), tiles of at most 32 KiB;
 // false when the shape does not fit.
-bool blk_ring_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
-    if (a.fmt != QR_FMT_Q8_0 || reinterpret_cast<uintptr_t>(a.x) % 16 || a.cols % 64 ||
-        reinterpret_cast<uintptr_t>(a.w) % 4 || a.row_bytes % 4)
-        return false;
+// Workgroups of a group launch: `budget` split over the matrices in proportion to their
+// tiles (at least one each, at most one per tile), doubled while the terms of a workgroup's
+// tiles (`per_tile` bytes each, after `fixed` bytes) exceed `target` bytes of LDS.  Returns
+// the LDS bytes; start[] gets the workgroup ranges.
+size_t group_grid(BlkGroup& gr, int budget, size_t fixed, size_t per_tile, size_t target) {
+    long long total = 0;
+    for (int m = 0; m < gr.n; ++m) total += gr.ntiles[m];
+    int G[kMatVecGroupMax];
+    for (int m = 0; m < gr.n; ++m)
+        G[m] = static_cast<int>(std::max<long long>(1, std::min<long long>(gr.ntiles[m], static_cast<long long>(budget) * gr.ntiles[m] / total)));
+    size_t lds = 0;
+    for (;;) {
+        int tpw = 1;
+        bool full = true;
+        for (int m = 0; m < gr.n; ++m) {
+            tpw = std::max(tpw, (gr.ntiles[m] + G[m] - 1) / G[m]);
+            full = full && G[m] == gr.ntiles[m];
+        }
+        lds = fixed + static_cast<size_t>(tpw) * per_tile;
+        if (lds <= target || full) break;
+        for (int m = 0; m < gr.n; ++m) G[m] = std::min(gr.ntiles[m], 2 * G[m]);
+    }
+    gr.start[0] = 0;
+    for (int m = 0; m < gr.n; ++m) gr.start[m + 1] = gr.start[m] + G[m];
+    return lds;
+}
+
+BlkGroup group_of(const MatVecArgs* a, int n, int R) {
+    BlkGroup gr{};
+    gr.n = n;
+    for (int m = 0; m < n; ++m) {
+        gr.w[m] = a[m].w;
+        gr.rows[m] = a[m].rows;
+        gr.y[m] = a[m].y;
+        gr.ntiles[m] = static_cast<int>((a[m].rows + R - 1) / R);
+    }
+    return gr;
+}
+
+// Q8_0 (block pairs, 4-byte aligned rows) in the ring form, for one matrix or a group that
+// shares x: false when the shape does not fit it.
+bool blk_ring_launch(const MatVecArgs* a, int n, hipStream_t stream, hipError_t* err) {
+    for (int m = 0; m < n; ++m)
+        if (a[m].fmt != QR_FMT_Q8_0 || reinterpret_cast<uintptr_t>(a[m].x) % 16 || a[m].cols % 64 ||
+            reinterpret_cast<uintptr_t>(a[m].w) % 4 || a[m].row_bytes % 4 || a[m].rows < 1)
+            return false;
     MvRing k{};
-    k.P = a.cols / 64;
+    k.P = a[0].cols / 64;
     if (k.P > 256) return false;
     k.tpg = k.P <= 64 ? 64 : k.P <= 128 ? 128 : 256;  // four waves always: U units per wave per tile
     k.rg = kMvThreads / k.tpg;
     k.R = k.rg;
-    const long long tile = static_cast<long long>(k.R) * a.row_bytes;
+    const long long tile = static_cast<long long>(k.R) * a[0].row_bytes;
     int U = static_cast<int>((tile + 4095) / 4096);
     if (U > 8) return false;
     if (U == 7) U = 8;
     k.slot_bytes = 4096 * U;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
-    k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
-    if (a.rows >= (1LL << 31) - k.R) return false;
-    // workgroups: two per CU when the LDS allows, the terms of all of a workgroup's tiles kept
-    int G = std::min(k.ntiles, 512);
-    size_t lds = 0;
-    for (;; G = std::min(k.ntiles, G * 2)) {
-        const int tpw = (k.ntiles + G - 1) / G;
-        lds = static_cast<size_t>(kRingSlots) * k.slot_bytes + static_cast<size_t>(tpw) * k.R * k.tstride * 4;
-        if (lds <= 80 * 1024 || G == k.ntiles) break;
+    long long groups_total = 0;
+    for (int m = 0; m < n; ++m) {
+        if (a[m].rows >= (1LL << 31) - k.R) return false;
+        groups_total += (a[m].rows + k.R - 1) / k.R;
     }
+    if (groups_total >= (1LL << 31)) return false;
+    BlkGroup gr = group_of(a, n, k.R);
+    k.ntiles = gr.ntiles[0];
+    // workgroups: two per CU when the LDS allows, the terms of all of a workgroup's tiles kept
+    const size_t lds = group_grid(gr, 512, static_cast<size_t>(kRingSlots) * k.slot_bytes,
+                                  static_cast<size_t>(k.R) * k.tstride * 4, 80 * 1024);
     if (lds > 160 * 1024) return false;
-    const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
+    const dim3 grid(static_cast<unsigned>(gr.start[n]), static_cast<unsigned>(a[0].nq));
     switch (U) {
-    case 1: case 2: *err = ring_launch_q8<2>(a, k, grid, lds, stream); break;
-    case 3: *err = ring_launch_q8<3>(a, k, grid, lds, stream); break;
-    case 4: *err = ring_launch_q8<4>(a, k, grid, lds, stream); break;
-    case 5: *err = ring_launch_q8<5>(a, k, grid, lds, stream); break;
-    case 6: *err = ring_launch_q8<6>(a, k, grid, lds, stream); break;
-    default: *err = ring_launch_q8<8>(a, k, grid, lds, stream); break;
+    case 1: case 2: *err = ring_launch_q8<2>(a[0], k, gr, grid, lds, stream); break;
+    case 3: *err = ring_launch_q8<3>(a[0], k, gr, grid, lds, stream); break;
+    case 4: *err = ring_launch_q8<4>(a[0], k, gr, grid, lds, stream); break;
+    case 5: *err = ring_launch_q8<5>(a[0], k, gr, grid, lds, stream); break;
+    case 6: *err = ring_launch_q8<6>(a[0], k, gr, grid, lds, stream); break;
+    default: *err = ring_launch_q8<8>(a[0], k, gr, grid, lds, stream); break;
     }
     return true;
 }
@@ -1194,36 +1287,41 @@ bool blk_ring_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
 // The persistent form for Q4_K (64-column items: rows of at most 512 items, 32768 columns) and
 // Q8_0 (block pairs: whole pairs and 4-byte aligned rows): false when the shape does not fit or
 // the terms of a workgroup's tiles would not fit in 64 KiB of LDS.
-bool blk_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* err) {
-    const bool q4k = a.fmt == QR_FMT_Q4_K, q8 = a.fmt == QR_FMT_Q8_0;
-    if (!(q4k || q8) || reinterpret_cast<uintptr_t>(a.x) % 16 || a.cols % 64) return false;
-    if (q4k && (reinterpret_cast<uintptr_t>(a.w) % 16 || a.row_bytes % 16)) return false;
-    if (q8 && (reinterpret_cast<uintptr_t>(a.w) % 4 || a.row_bytes % 4)) return false;
+bool blk_persistent_launch(const MatVecArgs* a, int n, hipStream_t stream, hipError_t* err) {
+    const bool q4k = a[0].fmt == QR_FMT_Q4_K, q8 = a[0].fmt == QR_FMT_Q8_0;
+    long long rows_total = 0;
+    for (int m = 0; m < n; ++m) {
+        if (!(q4k || q8) || a[m].fmt != a[0].fmt || reinterpret_cast<uintptr_t>(a[m].x) % 16 || a[m].cols % 64 ||
+            a[m].rows < 1)
+            return false;
+        if (q4k && (reinterpret_cast<uintptr_t>(a[m].w) % 16 || a[m].row_bytes % 16)) return false;
+        if (q8 && (reinterpret_cast<uintptr_t>(a[m].w) % 4 || a[m].row_bytes % 4)) return false;
+        rows_total += a[m].rows;
+    }
     MvBlkP k{};
-    k.P = a.cols / 64;
+    k.P = a[0].cols / 64;
     if (k.P > 512) return false;
     k.tpg = (k.P + 63) / 64 * 64;
     k.rg = std::max(1, kMvThreads / k.tpg);
     // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts;
-    // Q4_K matrices with fewer than 512 tiles of kBlkRptQ4k rows per thread take one row per
+    // Q4_K launches with fewer than 512 tiles of kBlkRptQ4k rows per thread take one row per
     // thread (twice the tiles: their runtime is the latency of a workgroup's few tiles)
     int rpt = 1;
-    if (q4k) rpt = (a.rows + k.rg * kBlkRptQ4k - 1) / (k.rg * kBlkRptQ4k) < 512 ? 1 : kBlkRptQ4k;
+    if (q4k) rpt = (rows_total + k.rg * kBlkRptQ4k - 1) / (k.rg * kBlkRptQ4k) < 512 ? 1 : kBlkRptQ4k;
     k.R = k.rg * rpt;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
-    k.ntiles = static_cast<int>((a.rows + k.R - 1) / k.R);
-    if (static_cast<long long>(k.R) * a.row_bytes >= (1LL << 31) || a.rows >= (1LL << 31) - k.R) return false;
+    for (int m = 0; m < n; ++m)
+        if (static_cast<long long>(k.R) * a[m].row_bytes >= (1LL << 31) || a[m].rows >= (1LL << 31) - k.R) return false;
+    if ((rows_total + k.R - 1) / k.R >= (1LL << 31)) return false;
+    BlkGroup gr = group_of(a, n, k.R);
+    k.ntiles = gr.ntiles[0];
     const int threads = k.rg * k.tpg;
     const int wg_per_cu = std::max(1, kBlkWgPerCu * 256 / threads);
     // LDS: the terms of the workgroup's tiles, or the padded copy of x that precedes them;
     // more workgroups (fewer tiles each) when the terms would not fit
-    int G = std::min(k.ntiles, 256 * wg_per_cu);
-    size_t lds = 0;
-    for (;; G = std::min(k.ntiles, 2 * G)) {
-        const int tpw = (k.ntiles + G - 1) / G;
-        lds = std::max(static_cast<size_t>(tpw) * k.R * k.tstride * 4, static_cast<size_t>(k.P) * kXRow * 4);
-        if (lds <= 160 * 1024 || G == k.ntiles) break;
-    }
+    const size_t xbytes = static_cast<size_t>(k.P) * kXRow * 4;
+    size_t lds = group_grid(gr, 256 * wg_per_cu, 0, static_cast<size_t>(k.R) * k.tstride * 4, 160 * 1024);
+    lds = std::max(lds, xbytes);
     if (lds > 160 * 1024) return false;
     const int which = q4k ? (rpt == 1 ? 1 : 2) : 0;
     const void* fns[3] = {reinterpret_cast<const void*>(&matvec_blk_persistent<PolQ8, 1>),
@@ -1235,10 +1333,13 @@ bool blk_persistent_launch(const MatVecArgs& a, hipStream_t stream, hipError_t* 
         if (*err != hipSuccess) return true;
         attr[which] = true;
     }
-    const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(a.nq));
-    if (which == 2) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, kBlkRptQ4k>), grid, dim3(threads), lds, stream, a, k);
-    else if (which == 1) hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, 1>), grid, dim3(threads), lds, stream, a, k);
-    else hipLaunchKernelGGL((matvec_blk_persistent<PolQ8, 1>), grid, dim3(threads), lds, stream, a, k);
+    const dim3 grid(static_cast<unsigned>(gr.start[n]), static_cast<unsigned>(a[0].nq));
+    if (which == 2)
+        hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, kBlkRptQ4k>), grid, dim3(threads), lds, stream, a[0], k, gr);
+    else if (which == 1)
+        hipLaunchKernelGGL((matvec_blk_persistent<PolQ4K, 1>), grid, dim3(threads), lds, stream, a[0], k, gr);
+    else
+        hipLaunchKernelGGL((matvec_blk_persistent<PolQ8, 1>), grid, dim3(threads), lds, stream, a[0], k, gr);
     *err = hipGetLastError();
     return true;
 }
@@ -1271,14 +1372,28 @@ bool matvec_shape_ok(int fmt, int cols) {
 }
 
 // The single-wave fp form needs 16-byte aligned rows and x.
+bool fp_wave_fits(const MatVecArgs& a) {
+    return reinterpret_cast<uintptr_t>(a.w) % 16 == 0 && a.row_bytes % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && a.cols % 8 == 0;
+}
+
+template <int FMT>
+hipError_t launch_fp_group(const MatVecArgs& a, const FwGroup& g, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(g.start[g.n]), static_cast<unsigned>(a.nq));
+    hipLaunchKernelGGL((matvec_fp_wave<FMT, 8>), grid, dim3(64), 0, stream, a, g);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_fp(const MatVecArgs& a, hipStream_t stream) {
-    if (reinterpret_cast<uintptr_t>(a.w) % 16 || a.row_bytes % 16 || reinterpret_cast<uintptr_t>(a.x) % 16 ||
-        a.cols % 8)
-        return launch_fmt<FMT>(a, stream);
-    const dim3 grid(static_cast<unsigned>((a.rows + 7) / 8), static_cast<unsigned>(a.nq));
-    hipLaunchKernelGGL((matvec_fp_wave<FMT, 8>), grid, dim3(64), 0, stream, a);
-    return hipGetLastError();
+    if (!fp_wave_fits(a)) return launch_fmt<FMT>(a, stream);
+    FwGroup g{};
+    g.n = 1;
+    g.start[1] = static_cast<int>((a.rows + 7) / 8);
+    g.w[0] = a.w;
+    g.rows[0] = a.rows;
+    g.y[0] = a.y;
+    return launch_fp_group<FMT>(a, g, stream);
 }
 
 hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
@@ -1290,17 +1405,59 @@ hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream) {
     case QR_FMT_Q4_0: return launch_fmt<QR_FMT_Q4_0>(a, stream);
     case QR_FMT_Q8_0: {
         hipError_t e;
-        if (blk_ring_launch(a, stream, &e)) return e;
-        if (blk_persistent_launch(a, stream, &e)) return e;
+        if (blk_ring_launch(&a, 1, stream, &e)) return e;
+        if (blk_persistent_launch(&a, 1, stream, &e)) return e;
         return launch_fmt<QR_FMT_Q8_0>(a, stream);
     }
     case QR_FMT_Q4_K: {
         hipError_t e;
-        if (blk_persistent_launch(a, stream, &e)) return e;
+        if (blk_persistent_launch(&a, 1, stream, &e)) return e;
         return launch_fmt<QR_FMT_Q4_K>(a, stream);
     }
     case QR_FMT_Q6_K: return launch_fmt<QR_FMT_Q6_K>(a, stream);
     default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec_group(const MatVecArgs* a, int n, hipStream_t stream) {
+    // F32/F16/BF16 rows in the single-wave form: one launch for the group
+    bool one = n > 1 && (a[0].fmt == QR_FMT_F32 || a[0].fmt == QR_FMT_F16 || a[0].fmt == QR_FMT_BF16);
+    long long wgs = 0;
+    for (int m = 0; one && m < n; ++m) {
+        one = fp_wave_fits(a[m]) && a[m].fmt == a[0].fmt && a[m].cols == a[0].cols &&
+              a[m].row_bytes == a[0].row_bytes && a[m].x == a[0].x && a[m].nq == a[0].nq && a[m].rows > 0;
+        wgs += (a[m].rows + 7) / 8;
+    }
+    if (!one && n > 1 && a[0].nq > 0) {
+        // Q8_0 / Q4_K matrices of one x: one launch of the ring or persistent form
+        bool same = true;
+        for (int m = 1; m < n; ++m)
+            same = same && a[m].fmt == a[0].fmt && a[m].cols == a[0].cols && a[m].row_bytes == a[0].row_bytes &&
+                   a[m].x == a[0].x && a[m].nq == a[0].nq;
+        hipError_t e = hipSuccess;
+        if (same && a[0].fmt == QR_FMT_Q8_0 && (blk_ring_launch(a, n, stream, &e) || blk_persistent_launch(a, n, stream, &e)))
+            return e;
+        if (same && a[0].fmt == QR_FMT_Q4_K && blk_persistent_launch(a, n, stream, &e)) return e;
+    }
+    if (!one || a[0].nq == 0 || wgs >= (1LL << 31)) {
+        for (int m = 0; m < n; ++m) {
+            const hipError_t e = launch_matvec(a[m], stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    FwGroup g{};
+    g.n = n;
+    for (int m = 0; m < n; ++m) {
+        g.w[m] = a[m].w;
+        g.rows[m] = a[m].rows;
+        g.y[m] = a[m].y;
+        g.start[m + 1] = g.start[m] + static_cast<int>((a[m].rows + 7) / 8);
+    }
+    switch (a[0].fmt) {
+    case QR_FMT_F32: return launch_fp_group<QR_FMT_F32>(a[0], g, stream);
+    case QR_FMT_F16: return launch_fp_group<QR_FMT_F16>(a[0], g, stream);
+    default: return launch_fp_group<QR_FMT_BF16>(a[0], g, stream);
     }
 }
 

@@ -21,5 +21,10 @@ struct MatVecArgs {
 // cols a multiple of 8 for F32/F16/BF16 (the lane sums then need no tail).
 bool matvec_shape_ok(int fmt, int cols);
 hipError_t launch_matvec(const MatVecArgs& a, hipStream_t stream);
+// n <= kMatVecGroupMax MatVecs that read the same x (same format, cols and nq): one launch
+// when the format streams rows in the single-wave form (F32/F16/BF16), else one per matrix;
+// every y equals launch_matvec's.
+constexpr int kMatVecGroupMax = 4;
+hipError_t launch_matvec_group(const MatVecArgs* a, int n, hipStream_t stream);
 
 }  // namespace qr

@@ -163,6 +163,40 @@ int qr_matvec_dev(const void* w_dev, int format, long long rows, int cols, int n
     return QR_OK;
 }
 
+int qr_matvec_group_dev(int n, const void* const* w_devs, const long long* rows, int format, int cols, int nq,
+                        const float* x_dev, float* const* y_devs, void* stream) {
+    clear_error();
+    QR_CHECK_ARG(n >= 1 && n <= kMatVecGroupMax, "group of %d matrices outside [1, %d]", n, kMatVecGroupMax);
+    QR_CHECK_ARG(w_devs && rows && y_devs, "null weight / rows / y array");
+    QR_CHECK_ARG(matvec_shape_ok(format, cols),
+                 "format %d cannot take rows of %d weights (whole blocks; a multiple of 8 for F32/F16/BF16)",
+                 format, cols);
+    QR_CHECK_ARG(nq >= 0 && nq <= 65535, "nq %d outside [0, 65535]", nq);
+    MatVecArgs a[kMatVecGroupMax] = {};
+    int live = 0;
+    for (int m = 0; m < n; ++m) {
+        QR_CHECK_ARG(w_devs[m] != nullptr, "null weight pointer %d", m);
+        QR_CHECK_ARG(reinterpret_cast<uintptr_t>(w_devs[m]) % 16 == 0, "weight pointer %d must be 16-byte aligned", m);
+        QR_CHECK_ARG(rows[m] >= 0 && rows[m] <= (1LL << 31) - 1, "rows[%d] = %lld outside [0, 2^31)", m, rows[m]);
+        if (rows[m] == 0 || nq == 0) continue;
+        QR_CHECK_ARG(y_devs[m] != nullptr, "null y pointer %d", m);
+        MatVecArgs& b = a[live++];
+        b.w = static_cast<const uint8_t*>(w_devs[m]);
+        b.fmt = format;
+        b.rows = rows[m];
+        b.cols = cols;
+        b.row_bytes = weight_row_bytes(format, cols);
+        b.nq = nq;
+        b.x = x_dev;
+        b.y = y_devs[m];
+    }
+    if (live == 0) return QR_OK;
+    QR_CHECK_ARG(x_dev != nullptr, "null x pointer");
+    QR_CHECK_ARG(reinterpret_cast<uintptr_t>(x_dev) % 16 == 0, "x must be 16-byte aligned");
+    QR_HIP(launch_matvec_group(a, live, static_cast<hipStream_t>(stream)));
+    return QR_OK;
+}
+
 int qr_matvec(const qr_weight* w, int nq, const float* x, float* y) {
     clear_error();
     QR_CHECK_ARG(w != nullptr, "null weight handle");

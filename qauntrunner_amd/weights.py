@@ -105,6 +105,25 @@ def mla_wuv_dev(kvb, fmt, heads, nope, vdim, kv_lora, u, out, stream=None) -> No
                                      _stream(stream)))
 
 
+def matvec_group_dev(ws, fmt, rows, cols, x, ys, stream=None) -> None:
+    """MatVecs of up to 4 weights against the same x in one launch where the format allows
+    (qr_matvec_group_dev): ys[m][b, r] = DotRow(ws[m] row r, x[b])."""
+    n = len(ws)
+    if not (len(rows) == n == len(ys)):
+        raise ValueError("ws, rows and ys must have the same length")
+    if x.numel() % cols:
+        raise ValueError(f"x holds {x.numel()} values, not a multiple of cols = {cols}")
+    nq = x.numel() // cols
+    for m in range(n):
+        if ys[m].numel() != nq * rows[m]:
+            raise ValueError(f"ys[{m}] holds {ys[m].numel()} values, expected {nq * rows[m]}")
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    rp = (ctypes.c_longlong * n)(*rows)
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    check(_lib.load().qr_matvec_group_dev(n, wp, rp, format_code(fmt), cols, nq, ctypes.c_void_p(x.data_ptr()), yp,
+                                          _stream(stream)))
+
+
 def matvec_dev(w, fmt, rows, cols, x, y, stream=None) -> None:
     """y[b, r] = DotRow(W row r, x[b]) on device tensors (DotKernels.cs:599-633)."""
     nq = x.numel() // cols

@@ -121,6 +121,26 @@ def test_projection_arguments_validate_before_device():
     assert L.qr_weight_create(ctypes.byref(h), 4, 4, 48, fake) == _lib.QR_ERR_INVALID_ARGUMENT and not h.value
 
 
+def test_matvec_group_arguments_validate_before_device():
+    L = qr.load()
+    null = ctypes.c_void_p()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced
+    ws = (ctypes.c_void_p * 5)(*([0x1000] * 5))
+    ys = (ctypes.c_void_p * 5)(*([0x2000] * 5))
+    rows = (ctypes.c_longlong * 5)(*([64] * 5))
+    err = _lib.QR_ERR_INVALID_ARGUMENT
+    assert L.qr_matvec_group_dev(0, ws, rows, 1, 256, 1, fake, ys, null) == err        # empty group
+    assert L.qr_matvec_group_dev(5, ws, rows, 1, 256, 1, fake, ys, null) == err        # more than 4
+    assert L.qr_matvec_group_dev(2, null, rows, 1, 256, 1, fake, ys, null) == err      # null arrays
+    assert L.qr_matvec_group_dev(2, ws, null, 1, 256, 1, fake, ys, null) == err
+    assert L.qr_matvec_group_dev(2, ws, rows, 1, 250, 1, fake, ys, null) == err        # cols not a multiple of 8
+    bad = (ctypes.c_void_p * 2)(0x1000, 0x1008)
+    assert L.qr_matvec_group_dev(2, bad, rows, 1, 256, 1, fake, ys, null) == err       # misaligned weight
+    neg = (ctypes.c_longlong * 2)(64, -1)
+    assert L.qr_matvec_group_dev(2, ws, neg, 1, 256, 1, fake, ys, null) == err
+    assert L.qr_matvec_group_dev(2, ws, rows, 1, 256, 1, ctypes.c_void_p(0x1004), ys, null) == err  # x alignment
+
+
 class _FakeTensor:
     """Just enough of a torch tensor for the device-argument checks."""
 

@@ -47,6 +47,27 @@ def test_matvec_bit_exact_per_format(gpu, fmt):
     assert_exact(got, want, fmt)
 
 
+@pytest.mark.parametrize("fmt", ["F32", "F16", "BF16", "Q8_0", "Q4_K"])
+@pytest.mark.parametrize("rows", [(512, 128, 128), (300, 13, 77, 8)])
+def test_matvec_group_matches_single_calls(gpu, fmt, rows):
+    """qr_matvec_group_dev: the matrices of one x (wq/wk/wv-like, and row counts that are not
+    multiples of 8) in one launch give each matrix's single-call y, bit for bit."""
+    code, cols, nq = quant.FMT[fmt], 1024, 2
+    raws = [quant.random_rows(code, r, cols, 70 + m, 0.05)[0] for m, r in enumerate(rows)]
+    x = dev(normal(79, (nq, cols)))
+    ws = [dev(raw.reshape(-1)) for raw in raws]
+    ys = [torch.full((nq, r), float("nan"), device="cuda") for r in rows]
+    qr.matvec_group_dev(ws, code, list(rows), cols, x, ys)
+    singles = [torch.empty((nq, r), device="cuda") for r in rows]
+    for m, r in enumerate(rows):
+        qr.matvec_dev(ws[m], code, r, cols, x, singles[m])
+    torch.cuda.synchronize()
+    for m in range(len(rows)):
+        assert_exact(ys[m].cpu().numpy(), singles[m].cpu().numpy(), f"{fmt} group member {m}")
+    want = np.stack([oracle.matvec(code, raws[1], cols, x[b].cpu().numpy()) for b in range(nq)])
+    assert_exact(ys[1].cpu().numpy(), want, f"{fmt} group member 1 vs the oracle")
+
+
 @pytest.mark.parametrize("fmt", ["F16", "Q8_0", "Q4_K"])
 def test_matvec_llama_8b_projection(gpu, fmt):
     """The 8B wq / wo shape: 4096 x 4096."""
