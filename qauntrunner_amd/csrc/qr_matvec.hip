@@ -1304,10 +1304,12 @@ bool blk_persistent_launch(const MatVecArgs* a, int n, hipStream_t stream, hipEr
     k.tpg = (k.P + 63) / 64 * 64;
     k.rg = std::max(1, kMvThreads / k.tpg);
     // rows per thread and tile: loads of two tiles in flight stay within the 63 that vmcnt counts;
-    // Q4_K launches with fewer than 512 tiles of kBlkRptQ4k rows per thread take one row per
-    // thread (twice the tiles: their runtime is the latency of a workgroup's few tiles)
+    // Q4_K launches with fewer than 1024 tiles of kBlkRptQ4k rows per thread take one row per
+    // thread (twice the tiles: their runtime is the latency of a workgroup's few tiles; at the
+    // 8B shape the wq/wk/wv group and wo: 46.4-47.1 us per layer against 47.4-49.8 with the
+    // bound at 512 tiles)
     int rpt = 1;
-    if (q4k) rpt = (rows_total + k.rg * kBlkRptQ4k - 1) / (k.rg * kBlkRptQ4k) < 512 ? 1 : kBlkRptQ4k;
+    if (q4k) rpt = (rows_total + k.rg * kBlkRptQ4k - 1) / (k.rg * kBlkRptQ4k) < 1024 ? 1 : kBlkRptQ4k;
     k.R = k.rg * rpt;
     k.tstride = (2 * k.P + 3) / 4 * 4 + 4;
     for (int m = 0; m < n; ++m)
