@@ -15,7 +15,7 @@ import numpy as np
 from . import _lib
 from ._lib import FORMATS, check
 
-__all__ = ["Weight", "row_bytes", "format_code", "mla_q_absorb_dev", "mla_wuv_dev", "matvec_dev"]
+__all__ = ["Weight", "row_bytes", "format_code", "mla_q_absorb_dev", "mla_wuv_dev", "matvec_dev", "matvec_group_dev"]
 
 
 def format_code(fmt) -> int:
@@ -89,9 +89,41 @@ def _stream(stream):
     return ctypes.c_void_p(getattr(stream, "cuda_stream", stream))
 
 
+def _f32_dev(t, what, numel=None, multiple=None) -> int:
+    """Checks an fp32 torch tensor handed to a *_dev projection before its address reaches a
+    kernel (the C ABI cannot see device sizes): on the GPU, contiguous, float32, and either
+    at least `numel` elements (an output: the call writes the first `numel`) or a whole
+    number of `multiple`-element rows (an input whose rows set the vector count).  Returns
+    the rows."""
+    if not getattr(t, "is_cuda", False):
+        raise ValueError(f"{what}: expected a tensor on the GPU")
+    if not t.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    if str(t.dtype) != "torch.float32":
+        raise ValueError(f"{what}: expected float32, got {t.dtype}")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{what}: {t.numel()} elements, the call writes {numel}")
+    if multiple is not None and (multiple <= 0 or t.numel() % multiple):
+        raise ValueError(f"{what}: {t.numel()} elements are not whole rows of {multiple}")
+    return t.numel() // multiple if multiple else 0
+
+
+def _weight_dev(w, fmt, rows, cols, what) -> None:
+    """A weight given as a raw torch tensor must be a contiguous GPU buffer holding `rows`
+    rows of `cols` weights in format `fmt` (a Weight or a store view carries its own size)."""
+    if hasattr(w, "is_cuda"):
+        if not w.is_cuda or not w.is_contiguous():
+            raise ValueError(f"{what}: expected a contiguous tensor on the GPU")
+        need = rows * row_bytes(fmt, cols)
+        if w.numel() * w.element_size() < need:
+            raise ValueError(f"{what}: {w.numel() * w.element_size()} bytes, {need} needed")
+
+
 def mla_q_absorb_dev(kvb, fmt, heads, nope, rope, vdim, kv_lora, q, q_tilde, stream=None) -> None:
     """q_tilde[b,h,:] = sum_j q[b,h,j] * W_kvb[h*(nope+vdim)+j, :] (StreamingEngine.cs:517-529)."""
-    nq = q.numel() // (heads * (nope + rope))
+    _weight_dev(kvb, fmt, heads * (nope + vdim), kv_lora, "kvb")
+    nq = _f32_dev(q, "q", multiple=heads * (nope + rope))
+    _f32_dev(q_tilde, "q_tilde", numel=nq * heads * kv_lora)
     check(_lib.load().qr_mla_q_absorb_dev(_dev(kvb), format_code(fmt), heads, nope, rope, vdim, kv_lora, nq,
                                           ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(q_tilde.data_ptr()),
                                           _stream(stream)))
@@ -99,7 +131,9 @@ def mla_q_absorb_dev(kvb, fmt, heads, nope, rope, vdim, kv_lora, q, q_tilde, str
 
 def mla_wuv_dev(kvb, fmt, heads, nope, vdim, kv_lora, u, out, stream=None) -> None:
     """out[b,h,j] = DotF32(W_kvb[h*(nope+vdim)+nope+j, :], u[b,h]) (StreamingEngine.cs:569-576)."""
-    nq = u.numel() // (heads * kv_lora)
+    _weight_dev(kvb, fmt, heads * (nope + vdim), kv_lora, "kvb")
+    nq = _f32_dev(u, "u", multiple=heads * kv_lora)
+    _f32_dev(out, "out", numel=nq * heads * vdim)
     check(_lib.load().qr_mla_wuv_dev(_dev(kvb), format_code(fmt), heads, nope, vdim, kv_lora, nq,
                                      ctypes.c_void_p(u.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                                      _stream(stream)))
@@ -111,12 +145,10 @@ def matvec_group_dev(ws, fmt, rows, cols, x, ys, stream=None) -> None:
     n = len(ws)
     if not (len(rows) == n == len(ys)):
         raise ValueError("ws, rows and ys must have the same length")
-    if x.numel() % cols:
-        raise ValueError(f"x holds {x.numel()} values, not a multiple of cols = {cols}")
-    nq = x.numel() // cols
+    nq = _f32_dev(x, "x", multiple=cols)
     for m in range(n):
-        if ys[m].numel() != nq * rows[m]:
-            raise ValueError(f"ys[{m}] holds {ys[m].numel()} values, expected {nq * rows[m]}")
+        _weight_dev(ws[m], fmt, rows[m], cols, f"ws[{m}]")
+        _f32_dev(ys[m], f"ys[{m}]", numel=nq * rows[m])
     wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
     rp = (ctypes.c_longlong * n)(*rows)
     yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
@@ -126,6 +158,8 @@ def matvec_group_dev(ws, fmt, rows, cols, x, ys, stream=None) -> None:
 
 def matvec_dev(w, fmt, rows, cols, x, y, stream=None) -> None:
     """y[b, r] = DotRow(W row r, x[b]) on device tensors (DotKernels.cs:599-633)."""
-    nq = x.numel() // cols
+    _weight_dev(w, fmt, rows, cols, "w")
+    nq = _f32_dev(x, "x", multiple=cols)
+    _f32_dev(y, "y", numel=nq * rows)
     check(_lib.load().qr_matvec_dev(_dev(w), format_code(fmt), rows, cols, nq, ctypes.c_void_p(x.data_ptr()),
                                     ctypes.c_void_p(y.data_ptr()), _stream(stream)))

@@ -175,6 +175,30 @@ def test_device_tensor_arguments_are_checked_on_the_host():
             _dev_tensor(t, 8, code, "x")
 
 
+def test_projection_tensors_are_checked_on_the_host():
+    from qauntrunner_amd.weights import _f32_dev, _weight_dev
+
+    assert _f32_dev(_FakeTensor(12), "x", multiple=4) == 3
+    assert _f32_dev(_FakeTensor(12), "y", numel=12) == 0
+    assert _f32_dev(_FakeTensor(16), "y", numel=12) == 0               # a larger output buffer
+    for t, kw in ((_FakeTensor(13), {"multiple": 4}),                  # not whole rows
+                  (_FakeTensor(11), {"numel": 12}),                    # short output
+                  (_FakeTensor(12, cuda=False), {"numel": 12}),        # host tensor
+                  (_FakeTensor(12, contiguous=False), {"numel": 12}),  # strided view
+                  (_FakeTensor(12, "torch.float16"), {"numel": 12})):  # wrong element type
+        with pytest.raises(ValueError):
+            _f32_dev(t, "x", **kw)
+
+    class _Raw(_FakeTensor):
+        def element_size(self):
+            return 1
+    _weight_dev(_Raw(64 * 1024 * 2, "torch.uint8"), "F16", 64, 1024, "w")  # 64 rows of 2 KiB: enough
+    with pytest.raises(ValueError):
+        _weight_dev(_Raw(64 * 1024 * 2 - 1, "torch.uint8"), "F16", 64, 1024, "w")
+    with pytest.raises(ValueError):
+        _weight_dev(_Raw(64 * 1024 * 2, "torch.uint8", cuda=False), "F16", 64, 1024, "w")
+
+
 def test_device_position_tensors_are_checked_on_the_host():
     from qauntrunner_amd.caches import _dev_int32
 

@@ -160,8 +160,9 @@ def test_matvec_host_weight_and_errors(gpu):
         qr.matvec_dev(buf, 5, 96, 512, xs, y)             # Q2_K is not decoded here
     with pytest.raises(qr.QrInvalidArgument):
         qr.matvec_dev(buf, 4, 96, 500, xs, y)             # not whole Q8_0 blocks
+    padded = dev(np.concatenate([raw.reshape(-1), np.zeros(2, np.uint8)]))
     with pytest.raises(qr.QrInvalidArgument):
-        qr.matvec_dev(buf[2:], 4, 96, 512, xs, y)         # misaligned weights
+        qr.matvec_dev(padded[2:], 4, 96, 512, xs, y)      # misaligned weights (all rows inside the buffer)
     with pytest.raises(qr.QrInvalidArgument):
         qr.matvec_dev(buf, 1, 8, 12, dev(np.zeros(12, np.float32)), y)   # F16 cols not a multiple of 8
     qr.matvec_dev(buf, 4, 0, 512, xs, y)                  # zero rows: nothing to do

@@ -101,8 +101,11 @@ def test_zero_queries_and_errors(gpu):
         qr.mla_q_absorb_dev(kvb, 2, 2, 4, 0, 4, 60, q, qt)          # kv_lora not a multiple of 8
     with pytest.raises(qr.QrInvalidArgument):
         qr.mla_q_absorb_dev(kvb, 4, 2, 4, 0, 4, 48, q, qt)          # Q8_0 needs 32-weight blocks
+    padded = dev(np.concatenate([raw.reshape(-1), np.zeros(2, np.uint8)]))
     with pytest.raises(qr.QrInvalidArgument):
-        qr.mla_wuv_dev(kvb[2:], 2, 2, 4, 4, 64, dev(normal(2, (2, 64))), qt)  # misaligned kvb
+        qr.mla_wuv_dev(padded[2:], 2, 2, 4, 4, 64, dev(normal(2, (2, 64))), qt)  # misaligned kvb
+    with pytest.raises(ValueError):
+        qr.mla_wuv_dev(kvb, 2, 2, 4, 4, 64, dev(normal(2, (2, 64))), qt[:1, :3])  # output too short
 
 
 def _layer_inputs(heads, nope, rope, vdim, kv_lora, n, dtype, fmt, seed):
