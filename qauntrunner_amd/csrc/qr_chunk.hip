@@ -107,7 +107,9 @@ __device__ __forceinline__ int chunk_split_tokens(const ChunkK& p, int pos0) {
 // BF16: cache element type; NT: 16-row N tiles per wave; NSTAGE: LDS tile buffers;
 // QSPLIT: q is not exact in the cache type and enters as hi + lo parts.
 template <bool BF16, int D, int NT, int NSTAGE, bool QSPLIT>
-__global__ void __launch_bounds__(256, NT <= 2 ? 2 : 1) chunk_tile_kernel(const ChunkK p) {
+// Workgroups per CU: two at NT <= 2 with two LDS stages (64 KiB); one with three stages
+// (96 KiB of LDS) or NT = 4 (registers).
+__global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_tile_kernel(const ChunkK p) {
     using T = typename std::conditional<BF16, __bf16, _Float16>::type;
     typedef T vec8 __attribute__((ext_vector_type(8)));
     constexpr int NK = D / 32;               // QK k-steps
