@@ -10,7 +10,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libqr_attn.so")
+# QR_ATTN_LIB selects another build of the same library (the sanitizer builds of the host code)
+LIB_PATH = os.environ.get("QR_ATTN_LIB") or os.path.join(_HERE, "libqr_attn.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "qr_attn.h")
 
 PAGE_TOKENS = 256

@@ -93,7 +93,6 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherArgs a) {
 // rounded as in the reference (x0 c - x1 s, x0 s + x1 c).
 constexpr int kRopeRows = 1;
 constexpr int kVTileTpt = 8;       // V tile: tokens per thread (one 16-byte chunk per dim)
-constexpr int kRopeThreads = 256;  // threads per position workgroup and per V tile
 
 // 4 consecutive dims of one cache row: one 16- or 8-byte store when the plane is
 // token-major, element stores when it is dims-major.
@@ -374,7 +373,7 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
     const int D = a.app.geom.head_dim;
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
-    const int ipt = (heads * (D / 8) + kRopeThreads - 1) / kRopeThreads;
+    const int ipt = rope_items_per_thread(heads, D);
     // V tiles: 16-bit dims-major V plane (head_dim 64 or 128), kVTileTpt tokens per thread
     const bool tiles = a.app.geom.v_dims_major && a.app.geom.planes == 2 && (D == 64 || D == 128) &&
                        a.app.dtype != QR_DTYPE_F32;

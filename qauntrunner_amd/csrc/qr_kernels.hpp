@@ -100,6 +100,15 @@ struct RopeAppendArgs {
     float freq[kMaxRopeHalf];
 };
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream);
+// One workgroup of kRopeThreads threads per position, each thread taking up to
+// kRopeMaxItems items of 8 dims (K heads plus q heads); wider rows use a row kernel that
+// cannot read the position on the device, so device-position RoPE appends need
+// rope_items_per_thread(...) <= kRopeMaxItems.
+constexpr int kRopeThreads = 256;
+constexpr int kRopeMaxItems = 8;
+inline int rope_items_per_thread(int heads, int head_dim) {
+    return (heads * (head_dim / 8) + kRopeThreads - 1) / kRopeThreads;
+}
 
 // Widens 16-bit rows to fp32 (exact) -- used for 16-bit query inputs.
 hipError_t launch_widen(const void* src, int src_dtype, float* dst, long long n, hipStream_t stream);

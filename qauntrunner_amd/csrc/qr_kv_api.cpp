@@ -64,24 +64,40 @@ int check_resident(const qr_kv* kv, int seq_id, int layer, int pos) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 // Host view of the page accounting and SeqLen, read back from the device after
-// device-side appends (a no-op otherwise).
-int sync_host(const qr_kv* ckv) {
+// device-side appends (a no-op otherwise).  A device-pointer call enqueued under stream
+// capture skips the read-back (it would wait for the device): its checks then use the
+// host accounting, which never runs ahead of the device's (pages and SeqLen only grow
+// on the device), so they can reject a position the device already holds but never
+// accept one it does not.
+int sync_host(const qr_kv* ckv, hipStream_t stream = nullptr, bool device_call = false) {
     qr_kv* kv = const_cast<qr_kv*>(ckv);
     if (!kv->store.device_ahead()) return QR_OK;
+    if (device_call && capturing(stream)) return QR_OK;
     DeviceGuard dg(kv->device);
     return kv->store.pull(kv->seq_len);
+}
+
+// A call enqueued under stream capture leaves the addresses of the pool, the split
+// workspace and the position buffer in the graph: from then on the pool never moves
+// (growing it is an error) and a workspace that grows keeps its old allocation alive
+// for the graph's replays until the handle is destroyed.
+void note_capture(qr_kv* kv, hipStream_t stream) {
+    if (!capturing(stream)) return;
+    kv->store.freeze();
+    kv->workspace.keep_retired();
+    kv->steppos.keep_retired();
 }
 
 // Device copy of the accounting after host-side changes (once device-side appends are in use).
 int sync_device(qr_kv* kv, hipStream_t stream) {
     if (!kv->device_steps) return QR_OK;
     return kv->store.push(kv->seq_len, stream);
-}
-
-bool capturing(hipStream_t stream) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 // Appends rows already on the device (src_dtype, row stride kv_dim).
@@ -136,6 +152,16 @@ int rope_append_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, float* q,
     return sync_device(kv, stream);
 }
 
+// The split workspace may only grow outside stream capture.
+int grow_workspace(qr_kv* kv, size_t bytes, hipStream_t st) {
+    const size_t ws = std::max<size_t>(bytes, 256);
+    if (ws > kv->workspace.size()) {
+        QR_CHECK_ARG(!capturing(st), "the split workspace must grow to %zu bytes: make one call outside capture first", ws);
+        QR_TRY(kv->workspace.ensure(ws));
+    }
+    return QR_OK;
+}
+
 // Runs decode entries (seq_ids[i], seq_len[i]) with device q/out rows.
 int decode_dev(qr_kv* kv, int n, const int* seq_ids, const int* seq_len, int layer, const float* q,
                float* out, float scale, hipStream_t stream) {
@@ -157,7 +183,7 @@ int decode_dev(qr_kv* kv, int n, const int* seq_ids, const int* seq_len, int lay
             a.pt_off[i] = kv->store.pt_offset(seq_ids[i0 + i], layer);
         }
         const DecodePlan plan = plan_decode(a);
-        QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+        QR_TRY(grow_workspace(kv, plan.workspace_bytes, stream));
         QR_HIP(launch_decode(a, plan, kv->workspace.get(), stream, kv->split_event));
     }
     return QR_OK;
@@ -321,7 +347,8 @@ int qr_kv_append_range_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, co
                            const void* v_dev, int src_dtype, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
-    QR_TRY(sync_host(kv));
+    QR_TRY(sync_host(kv, as_stream(stream), true));
+    note_capture(kv, as_stream(stream));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
@@ -363,7 +390,8 @@ int qr_kv_append_rope_dev(qr_kv* kv, int seq_id, int layer, int pos0, int n, flo
                           const float* v_dev, float theta, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
-    QR_TRY(sync_host(kv));
+    QR_TRY(sync_host(kv, as_stream(stream), true));
+    note_capture(kv, as_stream(stream));
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(n >= 0, "negative row count %d", n);
     QR_CHECK_ARG(n == 0 || (k_dev && v_dev), "null k/v rows");
@@ -404,7 +432,8 @@ int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const i
                         float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
-    QR_TRY(sync_host(kv));
+    QR_TRY(sync_host(kv, as_stream(stream), true));
+    note_capture(kv, as_stream(stream));
     QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
     std::vector<int> seq_len;
     QR_TRY(validate_batch(kv, n, seq_ids, layer, pos, seq_len));
@@ -416,7 +445,8 @@ int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer,
                                 const float* q_dev, float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
-    QR_TRY(sync_host(kv));
+    QR_TRY(sync_host(kv, as_stream(stream), true));
+    note_capture(kv, as_stream(stream));
     QR_CHECK_ARG(q_dev && attn_dev, "null q/attn pointer");
     QR_CHECK_ARG(n >= 1 && n <= kMaxDecodeBatch, "batch size %d outside [1, %d] for the no-allocation call", n,
                  kMaxDecodeBatch);
@@ -490,7 +520,7 @@ int chunk_common(qr_kv* kv, int seq_id, int layer, int pos0, int nq, const void*
         c.out = dout;
         c.scale = scale;
         const ChunkPlan plan = plan_chunk(c);
-        QR_TRY(kv->workspace.ensure(std::max<size_t>(plan.workspace_bytes, 256)));
+        QR_TRY(grow_workspace(kv, plan.workspace_bytes, stream));
         QR_HIP(launch_chunk(c, plan, kv->workspace.get(), stream, kv->split_event));
     } else {
         // exact fp32 path: every query is one decode entry with its causal length; the
@@ -525,7 +555,8 @@ int qr_kv_attention_chunk_dev(qr_kv* kv, int seq_id, int layer, int pos0, int nq
                               int q_dtype, float* attn_dev, float scale, void* stream) {
     clear_error();
     QR_TRY(check_handle(kv));
-    QR_TRY(sync_host(kv));
+    QR_TRY(sync_host(kv, as_stream(stream), true));
+    note_capture(kv, as_stream(stream));
     return chunk_common(kv, seq_id, layer, pos0, nq, q_dev, q_dtype, attn_dev, true, true, scale,
                         as_stream(stream));
 }
@@ -653,24 +684,20 @@ int qr_kv_read(qr_kv* kv, int seq_id, int layer, int pos0, int n, void* k_out, v
 
 namespace {
 
-// The split workspace may only grow outside stream capture.
-int grow_workspace(qr_kv* kv, size_t bytes, hipStream_t st) {
-    const size_t ws = std::max<size_t>(bytes, 256);
-    if (ws > kv->workspace.size()) {
-        QR_CHECK_ARG(!capturing(st), "the split workspace must grow to %zu bytes: make one call outside capture first", ws);
-        QR_TRY(kv->workspace.ensure(ws));
-    }
-    return QR_OK;
-}
-
 // Ensure + RoPE + Append of n rows at the device positions *pos_dev .. *pos_dev + n - 1
 // (the single-position and the chunk step calls).
 int rope_step_dev(qr_kv* kv, int seq_id, int layer, int n, const int* pos_dev, float* q_dev, const float* k_dev,
                   const float* v_dev, float theta, hipStream_t st) {
     QR_TRY(check_seq_layer(kv, seq_id, layer));
     QR_CHECK_ARG(pos_dev && k_dev && v_dev, "null pos/k/v pointer");
+    // checked before the page claim is enqueued: a rejected append must leave the
+    // device accounting as it was
+    QR_CHECK_ARG(rope_items_per_thread(kv->kv_heads + (q_dev ? kv->heads : 0), kv->head_dim) <= kRopeMaxItems,
+                 "device-position RoPE appends take at most %d dims of K and q per position (got %d)",
+                 kRopeThreads * kRopeMaxItems * 8, (kv->kv_heads + (q_dev ? kv->heads : 0)) * kv->head_dim);
     DeviceGuard dg(kv->device);
     const bool cap = capturing(st);
+    note_capture(kv, st);
     if (!kv->device_steps) {
         // first device-side append: the device copy starts from the host accounting
         QR_CHECK_ARG(!cap, "the first device-side append of a cache must run outside stream capture");
@@ -771,6 +798,7 @@ int qr_kv_attention_step_dev(qr_kv* kv, int n, const int* seq_ids, int layer, co
                  kMaxDecodeBatch);
     QR_CHECK_ARG(seq_ids, "null seq_ids array");
     DeviceGuard dg(kv->device);
+    note_capture(kv, as_stream(stream));
     return attention_step(kv, n, seq_ids, layer, pos_dev, q_dev, attn_dev, scale, as_stream(stream));
 }
 
@@ -784,6 +812,7 @@ int qr_kv_attention_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, con
     QR_CHECK_ARG(nq >= 1 && nq <= kv->max_seq, "nq %d outside [1, %d]", nq, kv->max_seq);
     DeviceGuard dg(kv->device);
     const hipStream_t st = as_stream(stream);
+    note_capture(kv, st);
     QR_CHECK_ARG(kv->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
     if (chunk_mfma_eligible(kv->dtype, kv->head_dim, kv->heads, kv->kv_heads)) {
         ChunkArgs c{};

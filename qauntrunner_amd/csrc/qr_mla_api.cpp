@@ -57,10 +57,18 @@ int check_resident(const qr_mla* m, int layer, int pos) {
 }
 
 // Host view of the page accounting and SeqLen, read back from the device after
-// device-side appends (a no-op otherwise).
-int sync_host(const qr_mla* cm) {
+// device-side appends (a no-op otherwise).  A device-pointer call enqueued under stream
+// capture skips the read-back (it would wait for the device): its checks then use the
+// host accounting, which never runs ahead of the device's.
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+int sync_host(const qr_mla* cm, hipStream_t stream = nullptr, bool device_call = false) {
     qr_mla* m = const_cast<qr_mla*>(cm);
     if (!m->store.device_ahead()) return QR_OK;
+    if (device_call && capturing(stream)) return QR_OK;
     DeviceGuard dg(m->device);
     std::vector<int> len{m->seq_len};
     const int st = m->store.pull(len);
@@ -68,15 +76,21 @@ int sync_host(const qr_mla* cm) {
     return st;
 }
 
+// A call enqueued under stream capture leaves the addresses of the pool, the split
+// workspace and the projection buffers in the graph: from then on the pool never moves
+// (growing it is an error) and a buffer that grows keeps its old allocation alive for
+// the graph's replays until the handle is destroyed.
+void note_capture(qr_mla* m, hipStream_t stream) {
+    if (!capturing(stream)) return;
+    m->store.freeze();
+    m->workspace.keep_retired();
+    m->proj.keep_retired();
+}
+
 // Device copy of the accounting after host-side changes (once device-side appends are in use).
 int sync_device(qr_mla* m, hipStream_t stream) {
     if (!m->device_steps) return QR_OK;
     return m->store.push(std::vector<int>{m->seq_len}, stream);
-}
-
-bool capturing(hipStream_t stream) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 // SeqLen changed on the host (Reset / Truncate): the device copy follows before the call returns.
@@ -315,7 +329,8 @@ int qr_mla_append_range_dev(qr_mla* m, int layer, int pos0, int n, const void* r
                             void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
-    QR_TRY(sync_host(m));
+    QR_TRY(sync_host(m, static_cast<hipStream_t>(stream), true));
+    note_capture(m, static_cast<hipStream_t>(stream));
     QR_TRY(check_layer(m, layer));
     QR_CHECK_ARG(dtype_valid(src_dtype), "unknown source dtype %d", src_dtype);
     QR_CHECK_ARG(n >= 0 && (rows_dev || n == 0), "null rows / negative count");
@@ -353,7 +368,8 @@ int qr_mla_attention_dev(qr_mla* m, int layer, int pos, int heads, const float* 
                          const float* q_rope_dev, float scale, float* u_dev, void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
-    QR_TRY(sync_host(m));
+    QR_TRY(sync_host(m, static_cast<hipStream_t>(stream), true));
+    note_capture(m, static_cast<hipStream_t>(stream));
     QR_CHECK_ARG(q_tilde_dev && u_dev && (q_rope_dev || m->rope == 0), "null q_tilde/q_rope/u pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     DeviceGuard dg(m->device);
@@ -391,7 +407,8 @@ int qr_mla_attend_absorbed_dev(qr_mla* m, int layer, int pos, int heads, int nop
                                const void* kvb_dev, int kvb_format, float* out_dev, void* stream) {
     clear_error();
     QR_TRY(check_handle(m));
-    QR_TRY(sync_host(m));
+    QR_TRY(sync_host(m, static_cast<hipStream_t>(stream), true));
+    note_capture(m, static_cast<hipStream_t>(stream));
     QR_CHECK_ARG(q_dev && out_dev, "null q / out pointer");
     QR_TRY(validate_attention(m, layer, pos, heads));
     DeviceGuard dg(m->device);
@@ -480,6 +497,7 @@ int qr_mla_append_step_dev(qr_mla* m, int layer, int n, const int* pos0_dev, con
     DeviceGuard dg(m->device);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const bool cap = capturing(st);
+    note_capture(m, st);
     if (!m->device_steps) {
         // first device-side append: the device copy starts from the host accounting
         QR_CHECK_ARG(!cap, "the first device-side append of a cache must run outside stream capture");
@@ -530,6 +548,7 @@ int qr_mla_attention_step_dev(qr_mla* m, int layer, const int* pos_dev, int head
     QR_CHECK_ARG(heads >= 1 && heads <= kMlaMaxHeads, "heads %d outside [1, %d]", heads, kMlaMaxHeads);
     QR_CHECK_ARG(m->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
     DeviceGuard dg(m->device);
+    note_capture(m, static_cast<hipStream_t>(stream));
     return attention_dev(m, layer, 0, pos_dev, heads, q_tilde_dev, q_rope_dev, scale, u_dev,
                          static_cast<hipStream_t>(stream));
 }
@@ -545,6 +564,7 @@ int qr_mla_attend_absorbed_step_dev(qr_mla* m, int layer, const int* pos_dev, in
     QR_CHECK_ARG(heads >= 1 && heads <= kMlaMaxHeads, "heads %d outside [1, %d]", heads, kMlaMaxHeads);
     QR_CHECK_ARG(m->store.capacity() >= 1, "the page pool is empty: nothing was appended or reserved");
     DeviceGuard dg(m->device);
+    note_capture(m, static_cast<hipStream_t>(stream));
     return attend_absorbed_dev(m, layer, 0, pos_dev, heads, nope, vdim, q_dev, kvb_dev, kvb_format, out_dev,
                                static_cast<hipStream_t>(stream));
 }

@@ -19,6 +19,7 @@
 #include <climits>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <new>
@@ -219,7 +220,7 @@ size_t env_size(const char* name, size_t dflt, size_t lo, size_t hi) {
     return (*end == '\0' && x >= lo && x <= hi) ? static_cast<size_t>(x) : dflt;
 }
 
-struct Chunk {
+struct ReadChunk {
     size_t slot_offset;
     long long file_offset;
     size_t bytes;
@@ -305,6 +306,10 @@ int parse_header(qr_model* m) {
     long long data_start = 8LL + hlen;
     long long explicit_start;
     if (as_int(root.get("data_offset"), &explicit_start)) data_start = explicit_start;
+    if (data_start > LLONG_MAX - 63) {  // the 64-byte rounding would overflow
+        set_error("%s: corrupt header (data_offset %lld past the end of the file)", m->path.c_str(), data_start);
+        return QR_ERR_INVALID_ARGUMENT;
+    }
     data_start = (data_start + 63) & ~63LL;
     if (data_start < 8LL + hlen) {
         set_error("%s: corrupt header (data_offset %lld < header end %lld)", m->path.c_str(), data_start,
@@ -335,14 +340,15 @@ int parse_header(qr_model* m) {
             }
             t.dims.push_back(v);
         }
-        t.format = static_cast<int>(fmt);
-        t.file_offset = data_start + off;
-        t.bytes = size;
         // the reference maps the file and would fault on such a tensor; here it is refused up front
-        if (t.file_offset + t.bytes > fsize) {
+        // (compared without forming data_start + offset + size, which can overflow)
+        if (off > fsize - data_start || size > fsize - data_start - off) {
             set_error("%s: tensor %s runs past the end of the file", m->path.c_str(), t.name.c_str());
             return QR_ERR_INVALID_ARGUMENT;
         }
+        t.format = static_cast<int>(std::max<long long>(INT_MIN, std::min<long long>(fmt, INT_MAX)));
+        t.file_offset = data_start + off;
+        t.bytes = size;
         auto it = m->index.find(t.name);
         if (it != m->index.end()) {
             m->tensors[it->second] = std::move(t);  // a repeated name replaces the earlier entry
@@ -364,6 +370,43 @@ bool read_exact(int fd, void* dst, long long bytes, long long offset) {
         offset += r;
     }
     return true;
+}
+
+// Reads `chunks` into host + slot_offset with up to `nthreads` threads (the caller's included)
+// taking chunks in file order.  `thread_init` runs once on every reading thread before its
+// first chunk, `after` on the reading thread after each chunk lands (the staging path queues
+// the chunk's upload there); either may be empty.  Returns false on a short read or when
+// either callback fails; the other readers stop before their next chunk.
+bool parallel_read(int fd, const std::vector<ReadChunk>& chunks, char* host, size_t nthreads,
+                   const std::function<bool()>& thread_init, const std::function<bool(const ReadChunk&)>& after) {
+    std::atomic<size_t> next{0};
+    std::atomic<bool> failed{false};
+    auto reader = [&]() {
+        if (thread_init && !thread_init()) {
+            failed = true;
+            return;
+        }
+        for (size_t i; !failed && (i = next.fetch_add(1)) < chunks.size();) {
+            const ReadChunk& c = chunks[i];
+            if (!read_exact(fd, host + c.slot_offset, static_cast<long long>(c.bytes), c.file_offset) ||
+                (after && !after(c))) {
+                failed = true;
+                return;
+            }
+        }
+    };
+    nthreads = std::max<size_t>(1, std::min(nthreads, chunks.size()));
+    std::vector<std::thread> pool;
+    for (size_t i = 1; i < nthreads; ++i) {
+        try {
+            pool.emplace_back(reader);
+        } catch (...) {
+            break;  // fewer readers
+        }
+    }
+    reader();
+    for (auto& t : pool) t.join();
+    return !failed;
 }
 
 int ensure_device(qr_model* m) {
@@ -438,7 +481,7 @@ void read_layer(qr_model* m, qr_model::Slot* s, int layer) {
     // file order, read each into the pinned buffer and queue its upload at once, so the file
     // reads run in parallel and overlap the host-to-device copies.
     std::map<std::string, size_t> offsets;
-    std::vector<Chunk> chunks;
+    std::vector<ReadChunk> chunks;
     size_t off = 0;
     for (const Tensor* t : list) {
         offsets[t->name] = off;
@@ -448,36 +491,17 @@ void read_layer(qr_model* m, qr_model::Slot* s, int layer) {
                               static_cast<size_t>(std::min<long long>(step, t->bytes - c))});
         off += align_up(static_cast<size_t>(t->bytes));
     }
-    std::atomic<size_t> next{0};
-    std::atomic<bool> failed{false}, queued{false};
-    auto reader = [&]() {
-        if (hipSetDevice(m->device) != hipSuccess) {
-            failed = true;
-            return;
-        }
-        for (size_t i; !failed && (i = next.fetch_add(1)) < chunks.size();) {
-            const Chunk& c = chunks[i];
-            char* host = static_cast<char*>(s->pinned) + c.slot_offset;
-            if (!read_exact(m->fd, host, static_cast<long long>(c.bytes), c.file_offset) ||
-                hipMemcpyAsync(static_cast<char*>(s->dev) + c.slot_offset, host, c.bytes, hipMemcpyHostToDevice,
-                               s->stream) != hipSuccess) {
-                failed = true;
-                return;
-            }
+    std::atomic<bool> queued{false};
+    char* pinned = static_cast<char*>(s->pinned);
+    const bool ok = parallel_read(
+        m->fd, chunks, pinned, m->read_threads, [m]() { return hipSetDevice(m->device) == hipSuccess; },
+        [&](const ReadChunk& c) {
+            if (hipMemcpyAsync(static_cast<char*>(s->dev) + c.slot_offset, pinned + c.slot_offset, c.bytes,
+                               hipMemcpyHostToDevice, s->stream) != hipSuccess)
+                return false;
             queued = true;
-        }
-    };
-    const size_t nthreads = std::min<size_t>(m->read_threads, chunks.size());
-    std::vector<std::thread> pool;
-    for (size_t i = 1; i < nthreads; ++i) {
-        try {
-            pool.emplace_back(reader);
-        } catch (...) {
-            break;  // fewer readers
-        }
-    }
-    reader();
-    for (auto& t : pool) t.join();
+            return true;
+        });
     // stream order puts the uploads after the fences Begin placed on this copy stream
     if (queued) {
         if (hipEventRecord(s->copied, s->stream) != hipSuccess) {
@@ -486,7 +510,7 @@ void read_layer(qr_model* m, qr_model::Slot* s, int layer) {
         }
         s->copy_pending = true;
     }
-    if (failed) return;
+    if (!ok) return;
     s->offsets.swap(offsets);
     s->staged = true;
     std::lock_guard<std::mutex> g(m->stats_mu);
@@ -637,7 +661,12 @@ int qr_model_read(const qr_model* m, const char* name, void* dst, long long dst_
     QR_CHECK_ARG(t != nullptr, "tensor '%s' not found in %s", name, m->path.c_str());
     QR_CHECK_ARG(dst != nullptr || t->bytes == 0, "null destination");
     QR_CHECK_ARG(dst_bytes >= t->bytes, "tensor '%s' needs %lld bytes, buffer holds %lld", name, t->bytes, dst_bytes);
-    if (!read_exact(m->fd, dst, t->bytes, t->file_offset)) {
+    // large tensors are read in chunks by the prefetch readers, in parallel
+    std::vector<ReadChunk> chunks;
+    const long long step = static_cast<long long>(m->read_chunk);
+    for (long long c = 0; c < t->bytes; c += step)
+        chunks.push_back({static_cast<size_t>(c), t->file_offset + c, static_cast<size_t>(std::min<long long>(step, t->bytes - c))});
+    if (!parallel_read(m->fd, chunks, static_cast<char*>(dst), m->read_threads, nullptr, nullptr)) {
         set_error("%s: short read of tensor %s", m->path.c_str(), name);
         return QR_ERR_INVALID_ARGUMENT;
     }

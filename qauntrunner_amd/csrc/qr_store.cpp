@@ -27,9 +27,18 @@ void clear_error() { g_last_error.clear(); }
 const char* last_error() { return g_last_error.c_str(); }
 
 // ---------------------------------------------------------------- DevBuf
+DevBuf::~DevBuf() {
+    if (ptr_) (void)hipFree(ptr_);
+    for (void* r : retired_) (void)hipFree(r);
+}
+
 int DevBuf::ensure(size_t bytes, bool zero) {
     if (bytes <= size_) return QR_OK;
-    if (ptr_) {
+    if (ptr_ && keep_retired_) {
+        retired_.push_back(ptr_);  // a captured graph may still use it: freed with the buffer
+        ptr_ = nullptr;
+        size_ = 0;
+    } else if (ptr_) {
         QR_HIP(hipDeviceSynchronize());
         QR_HIP(hipFree(ptr_));
         ptr_ = nullptr;
@@ -96,6 +105,11 @@ int PagedStore::push(const std::vector<int>& seq_len, hipStream_t stream) {
 
 int PagedStore::grow(long long min_pages) {
     if (min_pages <= pool_cap_) return QR_OK;
+    if (frozen_) {
+        set_error("the page pool holds %lld pages and cannot grow to %lld: a captured graph uses its address "
+                  "(reserve the pages before capturing)", pool_cap_, min_pages);
+        return QR_ERR_OUT_OF_MEMORY;
+    }
     const long long cap = std::max(min_pages, std::max(pool_cap_ * 2, 16LL));
     const size_t pb = static_cast<size_t>(page_bytes());
     char* fresh = nullptr;

@@ -26,18 +26,24 @@ private:
 };
 
 // Growable device buffer.  Growing waits for the device to go idle first,
-// because work enqueued on any stream may still read the old allocation.
+// because work enqueued on any stream may still read the old allocation.  Once a
+// captured graph holds the buffer's address (keep_retired), growing no longer frees
+// the old allocation: it stays valid for the graph's replays until the buffer is
+// destroyed.
 class DevBuf {
 public:
-    ~DevBuf() { if (ptr_) (void)hipFree(ptr_); }
+    ~DevBuf();
     // zero: a new allocation is zero-filled before it is returned
     int ensure(size_t bytes, bool zero = false);
+    void keep_retired() { keep_retired_ = true; }
     void* get() const { return ptr_; }
     size_t size() const { return size_; }
 
 private:
     void* ptr_ = nullptr;
     size_t size_ = 0;
+    bool keep_retired_ = false;
+    std::vector<void*> retired_;
 };
 
 // Page pool of one cache: `seqs` sequences x `layers` layers, each with a row
@@ -52,6 +58,10 @@ public:
     // Makes positions 0..tokens-1 of (seq, layer) resident; uploads new page-table entries.
     int ensure(int seq, int layer, int tokens, hipStream_t stream);
     int reserve(int pages);
+    // A captured graph holds the pool's address: from now on the pool never moves, and
+    // growing past its capacity is an error (the caller reserves pages before capturing).
+    void freeze() { frozen_ = true; }
+    bool frozen() const { return frozen_; }
 
     int pages_held(int seq, int layer) const { return held_[static_cast<size_t>(seq) * layers_ + layer]; }
     bool resident(int seq, int layer, int pos) const {
@@ -99,6 +109,7 @@ private:
     int* state_dev_ = nullptr;
     std::vector<int> state_host_;
     bool device_ahead_ = false;
+    bool frozen_ = false;
 };
 
 }  // namespace qr

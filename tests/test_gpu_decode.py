@@ -338,21 +338,22 @@ def test_c2_llama8b_decode_32k(gpu, dtype):
 
 
 def test_c2_llama8b_decode_32k_batch16_fp16(gpu):
-    """Batch 16 with independent page tables (sequences appended round-robin by page)."""
+    """Batch 16 with independent page tables (sequences appended round-robin by page); every
+    sequence's Q and K carry RoPE at base 500000 (Q at position 32,767), as at batch 1."""
     heads, kv_heads, D, n, B = 32, 8, 128, 32768, 16
     seqs = []
     with qr.PagedKvCache(1, heads, kv_heads, D, n, kv_dtype="f16", max_batch=B) as kv:
         kv.Reserve(B * 128)
+        qs = []
         for b in range(B):
-            rng = np.random.default_rng(300 + b)
-            K = rng.standard_normal((n, kv_heads * D), dtype=np.float32).astype(np.float16)
-            V = rng.standard_normal((n, kv_heads * D), dtype=np.float32).astype(np.float16)
-            seqs.append((K, V))
+            q, K, V = rope_inputs(heads, kv_heads, D, n, 300 + 3 * b)
+            seqs.append((K.astype(np.float16), V.astype(np.float16)))
+            qs.append(q)
         for p0 in range(0, n, 4096):  # interleave so page tables are not contiguous runs
             for b in range(B):
                 kv.AppendRange(0, p0, seqs[b][0][p0:p0 + 4096].view(np.uint16),
                                seqs[b][1][p0:p0 + 4096].view(np.uint16), src_dtype="f16", seq_id=b)
-        q = normal(400, (B, heads * D))
+        q = np.stack(qs)
         pos = [n - 1] * B
         out = kv.AttentionBatch(0, list(range(B)), pos, q, 1 / math.sqrt(D))
         for b in (0, 9, 15):
@@ -379,32 +380,33 @@ def test_c4_llama70b_decode_128k_fp16(gpu):
 
 
 def test_c2_llama8b_decode_32k_batch16_fp32(gpu):
-    """Batch 16 of 32,768 fp32 tokens each, pages of the 16 sequences interleaved in the pool.
-    This batch takes the plan of 16 pages per split (8 splits per entry), the longest split
-    plan of the streaming kernel; single-sequence calls take 4 pages per split."""
+    """Batch 16 of 32,768 fp32 tokens each, pages of the 16 sequences interleaved in the pool,
+    Q and K with RoPE at base 500000 (Q at position 32,767).  This batch takes the plan of 16
+    pages per split (8 splits per entry), the longest split plan of the streaming kernel;
+    single-sequence calls take 4 pages per split."""
     import torch
 
     heads, kv_heads, D, n, B = 32, 8, 128, 32768, 16
-    kv_dim, chunk, scale = kv_heads * D, 4096, 1 / math.sqrt(D)
+    kv_dim, chunk, scale, theta = kv_heads * D, 4096, 1 / math.sqrt(D), 500000.0
     checked = (0, 7, 15)
-    g = torch.Generator(device=gpu)
-    g.manual_seed(600)
     host = {b: ([], []) for b in checked}
     with qr.PagedKvCache(1, heads, kv_heads, D, n, kv_dtype="f32", max_batch=B) as kv:
         kv.Reserve(B * 128)
         for p0 in range(0, n, chunk):  # interleave so page tables are not contiguous runs
             for b in range(B):
-                K = torch.randn(chunk, kv_dim, device=gpu, generator=g)
-                V = torch.randn(chunk, kv_dim, device=gpu, generator=g)
-                kv.AppendRangeDev(0, p0, K, V, seq_id=b)
+                seed = 600 + 1000 * b + 2 * (p0 // chunk)
+                K = oracle.rope_rows(normal(seed, (chunk, kv_dim)), D, p0, theta)
+                V = normal(seed + 1, (chunk, kv_dim))
+                kv.AppendRangeDev(0, p0, torch.from_numpy(K).to(gpu), torch.from_numpy(V).to(gpu), seq_id=b)
                 if b in host:
-                    host[b][0].append(K.cpu().numpy())
-                    host[b][1].append(V.cpu().numpy())
+                    host[b][0].append(K)
+                    host[b][1].append(V)
         torch.cuda.synchronize()
         assert kv.BytesUsed == B * 128 * 256 * kv_dim * 4 * 2
         ids, pos = list(range(B)), [n - 1] * B
         assert kv.DecodePlan(0, ids, pos) == (16 * 256, 8)
-        q = normal(601, (B, heads * D))
+        q = np.stack([oracle.rope_rows(normal(601 + b, (1, heads * D)), D, n - 1, theta).reshape(-1)
+                      for b in range(B)])
         out = kv.AttentionBatch(0, ids, pos, q, scale)
         for b in checked:
             K, V = np.concatenate(host[b][0]), np.concatenate(host[b][1])
@@ -443,11 +445,10 @@ def test_decode_fp32_sixteen_page_splits(gpu, D, heads, kv_heads):
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_split_merge_over_many_back_to_back_calls(gpu, dtype):
-    """The last split workgroup of each (entry, unit) merges the unit's splits inside the
-    kernel, reading partials written by workgroups on other XCDs.  Many calls queued back
-    to back on one handle (alternating layers and batch sizes, new queries each time, no
-    host synchronisation between them) must each match the oracle: a stale partial or a
-    counter left non-zero by an earlier call would show up as a mismatch."""
+    """Split partials of many calls queued back to back on one handle (alternating layers and
+    batch sizes, new queries each time, no host synchronisation between them): each call
+    must match the oracle, so a partial left over from an earlier call, or merged into the
+    wrong entry, shows up as a mismatch."""
     import torch
 
     heads, kv_heads, D, n = 32, 8, 128, 8192

@@ -423,3 +423,128 @@ def test_captured_mla_layer_step_replays_at_advancing_positions(gpu):
         for pg in range(A.PageCount(0)):
             assert np.array_equal(A.Page(0, pg), B.Page(0, pg)), f"page {pg}"
         Wt.close()
+
+
+def test_captured_step_keeps_its_buffers_when_host_calls_grow_them(gpu):
+    """A graph captured over device-position steps keeps the pool and workspace addresses it
+    was recorded with.  Host calls made between replays that need a larger split workspace
+    get a new one while the graph keeps the old allocation; a host append that would grow
+    the pool is refused (QrOutOfMemory) instead of moving the pool under the graph.  Every
+    replay still matches the host path."""
+    import torch
+
+    heads, kv_heads, D, max_seq, seqs = 8, 2, 128, 4096, 16
+    p0, steps, other = 500, 6, 2000
+    Q, K, V = _rows(1100, p0 + steps + 1, heads, kv_heads, D)
+    _, Ko, Vo = _rows(1200, other, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, max_seq) as A, \
+            qr.PagedKvCache(1, heads, kv_heads, D, max_seq, max_batch=seqs) as B:
+        for kv in (A, B):
+            kv.AppendRopeDev(0, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        for s in range(1, seqs):  # the other sequences are filled before the capture
+            B.AppendRangeDev(0, 0, dev(Ko), dev(Vo), seq_id=s)
+        pos_dev = torch.zeros(1, dtype=torch.int32, device=gpu)
+        qb, ob = torch.empty(heads * D, device=gpu), torch.empty(heads * D, device=gpu)
+        kb, vb = torch.empty(kv_heads * D, device=gpu), torch.empty(kv_heads * D, device=gpu)
+
+        def load(t):
+            pos_dev.fill_(t)
+            qb.copy_(dev(Q[t]))
+            kb.copy_(dev(K[t]))
+            vb.copy_(dev(V[t]))
+
+        def check(t):
+            qa, oa = dev(Q[t]), torch.empty(heads * D, device=gpu)
+            _host_step(torch, A, 0, t, qa, dev(K[t]), dev(V[t]), oa)
+            torch.cuda.synchronize()
+            want, got = oa.cpu().numpy(), ob.cpu().numpy()
+            assert float(np.max(np.abs(got - want))) <= 2e-6 * float(np.max(np.abs(want))), f"position {t}"
+
+        load(p0)
+        B.AppendRopeStepDev(0, pos_dev, qb, kb, vb, THETA)
+        B.AttentionStepDev(0, [0], pos_dev, qb, ob, scale)
+        torch.cuda.synchronize()
+        check(p0)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            B.AppendRopeStepDev(0, pos_dev, qb, kb, vb, THETA, stream=s)
+            B.AttentionStepDev(0, [0], pos_dev, qb, ob, scale, stream=s)
+        for i, t in enumerate(range(p0 + 1, p0 + steps + 1)):
+            if i == 1:
+                # 15 sequences of 2000 positions in one call: a larger split workspace
+                ids = list(range(1, seqs))
+                qo = dev(normal(1300, (len(ids), heads * D)))
+                oo = torch.empty_like(qo)
+                B.AttentionDev(0, ids, [other - 1] * len(ids), qo, oo, scale)
+                torch.cuda.synchronize()
+                assert torch.isfinite(oo).all()
+            if i == 2:
+                # growing the pool would move it under the graph: refused
+                with pytest.raises(QrOutOfMemory, match="captured graph"):
+                    B.Reserve(100000)
+            load(t)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            check(t)
+        assert B.SeqLen == p0 + steps + 1
+
+
+def test_device_rope_step_rejects_wide_rows_before_claiming_pages(gpu):
+    """(heads + kv_heads) * head_dim above 16384 dims per position cannot take a device
+    position: the call is refused on the host before the page claim is enqueued, so the
+    device accounting stays as it was."""
+    import torch
+
+    heads, kv_heads, D = 128, 8, 128
+    with qr.PagedKvCache(1, heads, kv_heads, D, 4096) as kv:
+        pos = torch.tensor([0], dtype=torch.int32, device=gpu)
+        q = torch.ones(heads * D, device=gpu)
+        k = torch.ones(kv_heads * D, device=gpu)
+        with pytest.raises(qr.QrInvalidArgument, match="dims of K and q"):
+            kv.AppendRopeStepDev(0, pos, q, k, k, THETA)
+        torch.cuda.synchronize()
+        assert kv.SeqLen == 0 and kv.BytesUsed == 0
+        kv.AppendRopeStepDev(0, pos, None, k, k, THETA)  # K only: 1024 dims
+        assert kv.SeqLen == 1
+
+
+def test_no_alloc_decode_is_captured_after_a_device_step(gpu):
+    """qr_kv_attention_dev_noalloc enqueued under capture right after a device-position
+    append does not read the device accounting back (that would wait for the device inside
+    the capture); its host-side checks use the host accounting.  Replays equal the eager
+    call."""
+    import torch
+
+    heads, kv_heads, D, p0 = 8, 2, 128, 700
+    Q, K, V = _rows(1400, p0 + 2, heads, kv_heads, D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    scale = 1.0 / np.sqrt(D)
+    with qr.PagedKvCache(1, heads, kv_heads, D, 4096) as kv:
+        kv.AppendRopeDev(0, 0, dev(Q[:p0]), dev(K[:p0]), dev(V[:p0]), THETA)
+        kv.Reserve(16)
+        pos_dev = torch.tensor([p0], dtype=torch.int32, device=gpu)
+        qs = dev(Q[p0])
+        kv.AppendRopeStepDev(0, pos_dev, qs, dev(K[p0]), dev(V[p0]), THETA)  # the device is now ahead
+        q = dev(Q[p0 - 1])
+        out = torch.empty(heads * D, device=gpu)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            kv.AttentionDevNoAlloc(0, [0], [p0 - 1], q, out, scale, stream=s)
+        want = torch.empty_like(out)
+        kv.AttentionDev(0, [0], [p0 - 1], q, want, scale)  # eager, after a read-back
+        for _ in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, want)
+        assert kv.SeqLen == p0 + 1
