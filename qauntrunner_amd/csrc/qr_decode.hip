@@ -75,7 +75,52 @@ struct DecodeK {
     int seq_len[kMaxDecodeBatch];
     int pt_off[kMaxDecodeBatch];
     const int* pos_dev;  // device positions (seq = pos + 1, clamped to [1, seq_len]) when set
+    // In-kernel split merge (null: decode_combine_kernel merges): one arrival counter per
+    // (entry, unit), zero between calls; the last workgroup of a unit to arrive merges it.
+    unsigned* counters;
+    // XCD-local slots: a 1-D grid where (entry, unit) pair p runs on launch slots b with
+    // b % 8 == p % 8, i.e. on one XCD, so its partials stay in that XCD's L2.
+    int xmap;
 };
+
+// Split, unit and entry of this workgroup.  Launch slot b runs on XCD b % 8 (the
+// dispatcher's round robin over the 8 XCDs); with xmap set the slots of XCD x take the
+// pairs x, x + 8, ... with their splits consecutive.  Correctness does not depend on where
+// a slot runs: the merge protocol below is coherent across XCDs.
+__device__ __forceinline__ void slot_coords(const DecodeK& p, int& split, int& unit, int& b) {
+    if (p.xmap) {
+        const int bid = blockIdx.x;
+        const int k = bid >> 3;
+        const int j = k / p.split_stride;
+        split = k - j * p.split_stride;
+        const int pair = (bid & 7) + 8 * j;
+        unit = pair % p.units;
+        b = pair / p.units;
+    } else {
+        split = blockIdx.x;
+        unit = blockIdx.y;
+        b = blockIdx.z;
+    }
+}
+
+// Values of a lane pair (lanes l and l ^ off) in every lane of the pair: lo = the lower
+// lane's, hi = the upper's.  off 16 and 32 take one v_permlane16/32_swap (no LDS).
+__device__ __forceinline__ void lane_pair(float x, int off, float& lo, float& hi) {
+    if (off == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else if (off == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const float o = __shfl_xor(x, off);
+        const bool upper = (threadIdx.x & off) != 0;
+        lo = upper ? o : x;
+        hi = upper ? x : o;
+    }
+}
 
 // Positions attended by entry b: seq_len[b], or a device position + 1 bounded by it.
 // Workgroup-uniform: the position is a scalar load (no kernel here writes positions).
@@ -100,6 +145,115 @@ __device__ __forceinline__ float exp2_or_zero(float x_minus_m, float m) {
     return m == -INFINITY ? 0.f : fast_exp2(x_minus_m);
 }
 
+// ---- in-kernel split merge (DecodeK::counters set)
+//
+// Every split workgroup stores its partial (unnormalised o, then max and sum) with
+// write-through device-scope stores, waits until they are complete, and adds itself to its
+// unit's arrival counter.  The workgroup that arrives last knows every other partial of the
+// unit is in memory: it invalidates the caches that may hold an older copy (device-scope
+// acquire), merges the unit's splits, writes the output and resets the counter for the
+// next call.  No workgroup waits for another, so any grid size and any placement is safe;
+// XCD-local slots only make the partials' round trip shorter.
+
+// A partial value, written through to device scope.
+__device__ __forceinline__ void store_partial(float* dst, float v) {
+    __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LSE merge of the nsplit partials of heads h0..h0+G-1 of entry b by one workgroup.  T
+// threads share a float4 column (T = 1, 2 or 4: lanes l, l ^ 32 and l ^ 16 of one wave),
+// each merging every T-th split online with all its loads of a batch issued at once (always
+// in range: no branch around them); the T parts are merged through lane swaps.
+__device__ __forceinline__ void merge_unit(const DecodeK& p, int b, int h0, int G, int nsplit) {
+    const int D = p.head_dim;
+    const int d4n = D >> 2;
+    const int ncol = G * d4n;
+    const size_t row0 = static_cast<size_t>(b) * p.heads + h0;
+    const float4* acc4 = reinterpret_cast<const float4*>(p.part_acc);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int T = ncol > 128 ? 1 : ncol > 64 ? 2 : 4;
+    const int part = T == 1 ? 0 : T == 2 ? lane >> 5 : lane >> 4;
+    const int cpw = 64 / T;  // columns per wave
+    constexpr int kB = 16;
+    for (int c0 = 0; c0 < ncol; c0 += kWaves * cpw) {
+        const int c = c0 + wave * cpw + (lane & (cpw - 1));
+        const bool active = c < ncol;
+        const int cc = active ? c : 0;
+        const int g = cc / d4n;
+        const int d4 = cc - g * d4n;
+        const size_t base = (row0 + g) * p.split_stride;
+        float m = -INFINITY, l = 0.f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = part; s0 < nsplit; s0 += T * kB) {
+            float4 a[kB];
+            float2 ml[kB];
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int sp = min(s0 + i * T, nsplit - 1);
+                a[i] = acc4[(base + sp) * d4n + d4];
+                ml[i] = p.part_ml[base + sp];
+            }
+            float mb = m;
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                if (s0 + i * T >= nsplit) ml[i] = make_float2(-INFINITY, 0.f);  // a repeated split
+                mb = fmaxf(mb, ml[i].x);
+            }
+            const float cm = exp2_or_zero(m - mb, m);
+            l *= cm;
+            o.x *= cm; o.y *= cm; o.z *= cm; o.w *= cm;
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const float w = exp2_or_zero(ml[i].x - mb, ml[i].x);
+                l = fmaf(ml[i].y, w, l);
+                o.x = fmaf(a[i].x, w, o.x);
+                o.y = fmaf(a[i].y, w, o.y);
+                o.z = fmaf(a[i].z, w, o.z);
+                o.w = fmaf(a[i].w, w, o.w);
+            }
+            m = mb;
+        }
+        // every lane takes part in the swaps (inactive columns carry m = -inf, l = 0)
+        for (int off = T == 4 ? 16 : 32; T > 1 && off <= 32; off <<= 1) {
+            float mlo, mhi, llo, lhi, xlo, xhi;
+            lane_pair(m, off, mlo, mhi);
+            lane_pair(l, off, llo, lhi);
+            const float M = fmaxf(mlo, mhi);
+            const float clo = exp2_or_zero(mlo - M, mlo), chi = exp2_or_zero(mhi - M, mhi);
+            l = llo * clo + lhi * chi;
+            lane_pair(o.x, off, xlo, xhi);
+            o.x = xlo * clo + xhi * chi;
+            lane_pair(o.y, off, xlo, xhi);
+            o.y = xlo * clo + xhi * chi;
+            lane_pair(o.z, off, xlo, xhi);
+            o.z = xlo * clo + xhi * chi;
+            lane_pair(o.w, off, xlo, xhi);
+            o.w = xlo * clo + xhi * chi;
+            m = M;
+        }
+        if (active && part == 0)
+            *reinterpret_cast<float4*>(p.out + (row0 + g) * D + d4 * 4) = make_float4(o.x / l, o.y / l, o.z / l, o.w / l);
+    }
+}
+
+// Called by every thread of a split workgroup after its partial stores.
+__device__ __forceinline__ void arrive_and_merge(const DecodeK& p, int b, int unit, int h0, int G, int nsplit) {
+    // the write-through partial stores are complete before the count moves
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ unsigned s_ticket;
+    unsigned* ctr = p.counters + static_cast<size_t>(b) * p.units + unit;
+    if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket != static_cast<unsigned>(nsplit - 1)) return;
+    if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // device-scope acquire: the partial loads below miss the vector L1 and any L2 line that
+    // may hold an older copy
+    asm volatile("buffer_inv sc1" ::: "memory");
+    merge_unit(p, b, h0, G, nsplit);
+}
+
 // DT: head_dim fixed at compile time (0: read from the arguments).
 template <typename KT, int GMAX, int DPL, int U, int DT>
 __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p) {
@@ -109,9 +263,8 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     constexpr int ESZ = 16 / EPC;   // bytes per element
     constexpr int UMAX = U;         // rows per token group per step
 
-    const int split = blockIdx.x;
-    const int unit = blockIdx.y;
-    const int b = blockIdx.z;
+    int split, unit, b;
+    slot_coords(p, split, unit, b);
     const int seq = entry_seq(p, b);
     const int split_tokens = entry_split_tokens(p, seq);
     const int nsplit = (seq + split_tokens - 1) / split_tokens;
@@ -172,13 +325,16 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     // cost 5% at batch 16).
     const int rot = (split * 7) % nsteps;
     auto step_t0 = [&](int st) { return t_begin + (st + rot < nsteps ? st + rot : st + rot - nsteps) * step_tokens; };
-    // t0: first row of the step (wave-uniform: a step never crosses a page)
-    auto issue = [&](int t0_in, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
+    // Page-table entry of the step starting at row t0: a scalar load through the constant
+    // address space (the table is not written while the kernel runs, so it stays a scalar
+    // load whatever else the kernel stores).
+    auto phys_of = [&](int t0_in) -> long long {
+        return reinterpret_cast<const __attribute__((address_space(4))) int*>(
+            reinterpret_cast<uintptr_t>(pt))[__builtin_amdgcn_readfirstlane(t0_in) >> kPageShift];
+    };
+    // t0: first row of the step (wave-uniform: a step never crosses a page); phys: its page
+    auto issue_at = [&](int t0_in, long long phys, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
         const int t0 = __builtin_amdgcn_readfirstlane(t0_in);
-        // constant address space: the page table is not written while the kernel runs,
-        // so the entry is a scalar load whatever else the kernel stores
-        const long long phys = reinterpret_cast<const __attribute__((address_space(4))) int*>(
-            reinterpret_cast<uintptr_t>(pt))[t0 >> kPageShift];
         const char* kbase = p.pool + (phys * p.page_elems + head_off +
                                       static_cast<long long>(t0 & (kPageTokens - 1)) * D) * ESZ;
         // one buffer resource over the step's K rows and V rows (both planes of the page):
@@ -287,20 +443,27 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     // (past the end it re-reads the step just computed, which L2 still holds), so
     // the compiler's load counting stays exact and each step waits only for its own
     // loads.
-    issue(step_t0(0), kbuf[0], vbuf[0]);
+    issue_at(step_t0(0), phys_of(step_t0(0)), kbuf[0], vbuf[0]);
     load_q();
 #pragma unroll
-    for (int i = 1; i < kPrefetch; ++i) issue(step_t0(min(i, nsteps - 1)), kbuf[i], vbuf[i]);
+    for (int i = 1; i < kPrefetch; ++i) {
+        const int t0 = step_t0(min(i, nsteps - 1));
+        issue_at(t0, phys_of(t0), kbuf[i], vbuf[i]);
+    }
     // Unrolled by the buffer count so every buffer index is a constant: step s0 + k is
-    // computed from buffer k while step s0 + k + kPrefetch is loaded into the buffer
-    // computed last (past the end, the step being computed is loaded again).  Exits only
-    // through the goto: the back-edge is steady state.
+    // computed from buffer k while step nxt(s0 + k) = s0 + k + kPrefetch is loaded into the
+    // buffer computed last (past the end, the step being computed is loaded again).  The
+    // page-table entry of each issued step is loaded one issue ahead, so its latency never
+    // holds the loads back.  Exits only through the goto: the back-edge is steady state.
+    auto nxt = [&](int i) { return i + kPrefetch < nsteps ? i + kPrefetch : i; };
+    long long ph_next = phys_of(step_t0(nxt(0)));
     for (int s0 = 0;; s0 += kStreamBuffers) {
 #pragma unroll
         for (int k = 0; k < kStreamBuffers; ++k) {
-            const int ahead = s0 + k + kPrefetch;
-            issue(step_t0(ahead < nsteps ? ahead : s0 + k), kbuf[(k + kPrefetch) % kStreamBuffers],
-                  vbuf[(k + kPrefetch) % kStreamBuffers]);
+            const long long ph = ph_next;
+            ph_next = phys_of(step_t0(nxt(s0 + k + 1)));
+            issue_at(step_t0(nxt(s0 + k)), ph, kbuf[(k + kPrefetch) % kStreamBuffers],
+                     vbuf[(k + kPrefetch) % kStreamBuffers]);
             // the loads leave before any use of the step being computed, so that waiting
             // for that step never holds back the next one
             __builtin_amdgcn_sched_barrier(0);
@@ -310,18 +473,24 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
     }
 streamed:
 
-    // ---- merge the token groups of the wave (lanes with equal `sub`)
+    // ---- merge the token groups of the wave (lanes with equal `sub`), lane pairs l and
+    // l ^ off exchanged through permlane swaps where off is 16 or 32
     for (int off = LPT; off < 64; off <<= 1) {
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
-            const float m2 = __shfl_xor(m[g], off);
-            const float l2 = __shfl_xor(l[g], off);
-            const float M = fmaxf(m[g], m2);
-            const float c1 = exp2_or_zero(m[g] - M, m[g]);
-            const float c2 = exp2_or_zero(m2 - M, m2);
-            l[g] = l[g] * c1 + l2 * c2;
+            float mlo, mhi, llo, lhi;
+            lane_pair(m[g], off, mlo, mhi);
+            lane_pair(l[g], off, llo, lhi);
+            const float M = fmaxf(mlo, mhi);
+            const float clo = exp2_or_zero(mlo - M, mlo);
+            const float chi = exp2_or_zero(mhi - M, mhi);
+            l[g] = llo * clo + lhi * chi;
 #pragma unroll
-            for (int e = 0; e < DPL; ++e) acc[g][e] = acc[g][e] * c1 + __shfl_xor(acc[g][e], off) * c2;
+            for (int e = 0; e < DPL; ++e) {
+                float alo, ahi;
+                lane_pair(acc[g][e], off, alo, ahi);
+                acc[g][e] = alo * clo + ahi * chi;
+            }
             m[g] = M;
         }
     }
@@ -362,12 +531,20 @@ streamed:
         const int h = h0 + g;
         if (nsplit == 1) {
             p.out[(row_base + h) * D + d] = o / L;
+        } else if (p.counters) {
+            const size_t slot = (row_base + h) * p.split_stride + split;
+            store_partial(&p.part_acc[slot * D + d], o);
+            if (d == 0) {
+                store_partial(&p.part_ml[slot].x, M);
+                store_partial(&p.part_ml[slot].y, L);
+            }
         } else {
             const size_t slot = (row_base + h) * p.split_stride + split;
             p.part_acc[slot * D + d] = o;
             if (d == 0) p.part_ml[slot] = make_float2(M, L);
         }
     }
+    if (p.counters && nsplit > 1) arrive_and_merge(p, b, unit, h0, G, nsplit);
 }
 
 // ---------------------------------------------------------------------------
@@ -391,10 +568,6 @@ streamed:
 // pre-multiplied per head by the power of two that brings its largest element to at
 // most 2^14 (exact), so fp16 never overflows; the scores are scaled back.
 constexpr int kMfmaGroup = 16;  // query heads per unit on the MFMA path
-#ifndef QR_MFMA_DECODE_BUFFERS
-#define QR_MFMA_DECODE_BUFFERS 2
-#endif
-constexpr int kMfmaBuffers = QR_MFMA_DECODE_BUFFERS;  // register buffers of the step pipeline
 
 #ifndef QR_MFMA_DECODE_WG_PER_CU
 #define QR_MFMA_DECODE_WG_PER_CU 2
@@ -410,9 +583,8 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     constexpr int NDT = D / 16;  // PV dim tiles
     constexpr int kStep = 32;    // positions per step
 
-    const int split = blockIdx.x;
-    const int unit = blockIdx.y;
-    const int b = blockIdx.z;
+    int split, unit, b;
+    slot_coords(p, split, unit, b);
     const int seq = entry_seq(p, b);
     const int split_tokens = entry_split_tokens(p, seq);
     const int t_begin = split * split_tokens;
@@ -445,25 +617,40 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     const int rot = (split * 7) % total_steps;
     auto step_t0 = [&](int st) { return t_begin + (st + rot < total_steps ? st + rot : st + rot - total_steps) * kStep; };
 
-    constexpr int NB = kMfmaBuffers;
-    U32x4 kb[NB][2][NK];
-    U32x4 vb[NB][NDT];
-    auto issue = [&](int st, int buf) {
-        const int t0 = step_t0(st);  // a step never crosses a page
-        const long long phys = pt[t0 >> kPageShift];
+    U32x4 kb[2][2][NK];
+    U32x4 vb[2][NDT];
+    // Page-table entry of step st: a scalar load through the constant address space (the
+    // table is not written while the kernel runs).
+    auto phys_of = [&](int st) -> long long {
+        return reinterpret_cast<const __attribute__((address_space(4))) int*>(
+            reinterpret_cast<uintptr_t>(pt))[__builtin_amdgcn_readfirstlane(step_t0(st)) >> kPageShift];
+    };
+    // Loads of step st into buffer buf: buffer loads from a wave-uniform base (the step's
+    // first K row and its V^T column block, in SGPRs) plus loop-invariant lane offsets, so
+    // no per-step vector address is built (a per-step address in registers that the
+    // previous step's loads were still writing made the compiler drain every load in
+    // flight at the loop head).
+    const uint32_t k_lane = static_cast<uint32_t>((krow * D + 8 * q4) * 2);
+    const uint32_t v_lane = static_cast<uint32_t>((n * kPageTokens + 8 * q4) * 2);
+    auto issue_at = [&](int st, long long phys, int buf) {
+        const int t0 = __builtin_amdgcn_readfirstlane(step_t0(st));  // a step never crosses a page
         const int slot0 = t0 & (kPageTokens - 1);
         const char* kp = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
         const char* vp = p.pool + (phys * p.page_elems + p.plane_elems + kblk + slot0) * 2;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kp), 0, 0x7FFFFFFF, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vp), 0, 0x7FFFFFFF, kBufferFlags);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int kk = 0; kk < NK; ++kk)
-                kb[buf][mt][kk] = load16(kp + ((krow + 4 * mt) * D + 32 * kk + 8 * q4) * 2);
+                kb[buf][mt][kk] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    rk, k_lane + static_cast<uint32_t>((4 * mt * D + 32 * kk) * 2), 0, 0));
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) vb[buf][dt] = load16(vp + ((16 * dt + n) * kPageTokens + 8 * q4) * 2);
+        for (int dt = 0; dt < NDT; ++dt)
+            vb[buf][dt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                rv, v_lane, static_cast<uint32_t>(16 * dt * kPageTokens * 2), 0));
     };
-    if (nst > 0) issue(wave, 0);
-    if (NB == 3 && nst > 0) issue(nst > 1 ? wave + kWaves : wave, 1);
+    if (nst > 0) issue_at(wave, phys_of(wave), 0);
 
     // ---- q of head h0 + n (zero for padding columns), log2 units, split into hi + lo
     const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
@@ -562,29 +749,27 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         }
     };
 
-    // ---- pipeline over this wave's steps with NB register buffers (NB - 1 steps in
-    // flight ahead of the one computed); every iteration issues the same loads (past
-    // the end it re-reads a step already loaded) so the compiler's load counting stays
-    // exact
+    // ---- pipeline over this wave's steps with two register buffers (one step in flight
+    // ahead of the one computed); every iteration issues the same loads (past the end it
+    // re-reads a step already loaded) so the compiler's load counting stays exact.  The
+    // loads of the next step leave before any MFMA of the current one (scheduling barrier)
+    // and the page-table entry of each issued step is loaded one issue ahead.
     auto gstep = [&](int i) { return wave + kWaves * min(i, nst - 1); };
-    if (NB == 2) {
-        for (int i = 0; i < nst; i += 2) {
-            issue(gstep(i + 1), 1);
+    if (nst > 0) {
+        long long ph_next = phys_of(gstep(1));
+        for (int i = 0;; i += 2) {
+            long long ph = ph_next;
+            ph_next = phys_of(gstep(i + 2));
+            issue_at(gstep(i + 1), ph, 1);
+            __builtin_amdgcn_sched_barrier(0);
             compute(gstep(i), 0);
             if (i + 1 >= nst) break;
-            issue(gstep(i + 2), 0);
-            compute(gstep(i + 1), 1);
-        }
-    } else {
-        for (int i = 0; i < nst; i += 3) {
-            issue(gstep(i + 2), 2);
-            compute(gstep(i), 0);
-            if (i + 1 >= nst) break;
-            issue(gstep(i + 3), 0);
+            ph = ph_next;
+            ph_next = phys_of(gstep(i + 3));
+            issue_at(gstep(i + 2), ph, 0);
+            __builtin_amdgcn_sched_barrier(0);
             compute(gstep(i + 1), 1);
             if (i + 2 >= nst) break;
-            issue(gstep(i + 4), 1);
-            compute(gstep(i + 2), 2);
         }
     }
 
@@ -620,12 +805,20 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         const int h = h0 + g;
         if (nsplit == 1) {
             p.out[(row_base + h) * D + d] = o / L;
+        } else if (p.counters) {
+            const size_t slot = (row_base + h) * p.split_stride + split;
+            store_partial(&p.part_acc[slot * D + d], o);
+            if (d == 0) {
+                store_partial(&p.part_ml[slot].x, M);
+                store_partial(&p.part_ml[slot].y, L);
+            }
         } else {
             const size_t slot = (row_base + h) * p.split_stride + split;
             p.part_acc[slot * D + d] = o;
             if (d == 0) p.part_ml[slot] = make_float2(M, L);
         }
     }
+    if (p.counters && nsplit > 1) arrive_and_merge(p, b, unit, h0, G, nsplit);
 }
 
 // Log-sum-exp merge of the split partials: one workgroup per (head, entry).
@@ -805,8 +998,8 @@ int units_of(const DecodeArgs& a, int* gmax) {
 
 }  // namespace
 
-// Split partials of qr_kv_attention_dev_noalloc: a fixed array in device memory, so the
-// call allocates nothing.  Each GPU holds its own copy until the process ends; in host
+// Scratch of qr_kv_attention_dev_noalloc (arrival counters, then split partials): a fixed
+// array in device memory, so the call allocates nothing.  Each GPU holds its own copy until the process ends; in host
 // code the array's name is not a device address, so its address is taken once per
 // device with hipGetSymbolAddress and only that address is used.
 static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
@@ -833,6 +1026,8 @@ int decode_scratch_address(int device, void** ptr) {
             set_error("hipGetSymbolAddress returned a null scratch address on device %d", device);
             return QR_ERR_HIP;
         }
+        // the arrival counters at the front start at zero (set up once per device, before any call)
+        QR_HIP(hipMemset(a, 0, kDecodeCounterBytes));
         addr[device] = a;
     }
     *ptr = addr[device];
@@ -843,6 +1038,8 @@ DecodePlan plan_decode(const DecodeArgs& a) {
     DecodePlan pl{};
     int gmax = 1;
     pl.units = units_of(a, &gmax);
+    const bool per_head = a.heads % a.geom.kv_heads != 0;
+    const int group = per_head ? 1 : a.heads / a.geom.kv_heads;
     int max_pages = 1;
     long long work = 0;  // (unit, page) items of the launch
     for (int i = 0; i < a.nb; ++i) {
@@ -865,6 +1062,18 @@ DecodePlan plan_decode(const DecodeArgs& a) {
     pl.workspace_bytes = pl.max_splits > 1
         ? static_cast<size_t>(a.nb) * a.heads * pl.max_splits * (static_cast<size_t>(a.geom.head_dim) * 4 + 8)
         : 0;
+    // In-kernel merge when the whole grid runs in one pass (every split workgroup resident at
+    // once, so the merge sits on the call's critical path) and a unit's partials are small
+    // (at most 1024 outputs per split); otherwise the combine kernel spreads the merge over
+    // the GPU.  Measured on MI355X, per call: 8B 32K decode fp32 50.8 vs 51.9 us, fp16 32.1
+    // vs 32.8 us, 70B 128K fp16 97.8 vs 98.0 us; at batch 16 (four passes) the combine
+    // kernel is faster.
+    const int pairs = pl.units * a.nb;
+    const int unit_heads = per_head ? 1 : std::min(gmax, group);
+    pl.fused = pl.max_splits > 1 && static_cast<long long>(pl.max_splits) * pairs <= cu_count() &&
+               unit_heads * a.geom.head_dim <= 1024 && pairs <= kDecodeCounters;
+    // XCD-local slots need whole XCD rounds of pairs with equal head counts
+    pl.xmap = pl.fused && pairs % 8 == 0 && (per_head || group % gmax == 0 || group < gmax);
     return pl;
 }
 
@@ -903,6 +1112,9 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
         k.pt_off[i] = a.pt_off[i];
     }
     k.pos_dev = a.pos_dev;
+    const bool fused = pl.fused && a.counters;
+    k.counters = fused ? a.counters : nullptr;
+    k.xmap = fused && pl.xmap;
     if (pl.max_splits > kMaxSplits) return hipErrorInvalidValue;
     const void* fn;
     if (uses_mfma(a)) {
@@ -914,10 +1126,11 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
         fn = select_kernel(a.dtype, gmax, a.geom.head_dim);
     }
     void* args[] = {&k};
-    hipError_t e = hipLaunchKernel(fn, dim3(pl.max_splits, k.units, a.nb), dim3(kThreads), args, 0, stream);
+    const dim3 grid = k.xmap ? dim3(pl.max_splits * k.units * a.nb) : dim3(pl.max_splits, k.units, a.nb);
+    hipError_t e = hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, stream);
     if (e != hipSuccess) return e;
     if (after_split && (e = hipEventRecord(after_split, stream)) != hipSuccess) return e;
-    if (pl.max_splits == 1) return hipSuccess;
+    if (pl.max_splits == 1 || fused) return hipSuccess;
     hipLaunchKernelGGL(decode_combine_kernel, dim3(a.heads, a.nb), dim3(kThreads), 0, stream, k);
     return hipGetLastError();
 }

@@ -134,6 +134,10 @@ struct DecodeArgs {
     // Device-side positions: when set, entry b attends positions 0..pos_dev[b] (read by
     // the kernels, clamped to [0, seq_len[b] - 1]); seq_len[b] then only bounds the plan.
     const int* pos_dev;
+    // kDecodeCounters arrival counters in device memory, zero before the first call (each
+    // call leaves the ones it used at zero), for plans that merge splits inside the split
+    // kernel; null: the combine kernel merges.  Calls that share counters must not overlap.
+    unsigned* counters;
 };
 
 // Split-K plan for one launch.
@@ -142,7 +146,11 @@ struct DecodePlan {
     int max_splits;    // splits of the longest entry
     int units;         // workgroups per (entry, split): kv heads x head chunks, or heads
     size_t workspace_bytes;  // split partials
+    int fused;         // splits merged inside the split kernel (needs DecodeArgs::counters)
+    int xmap;          // XCD-local launch slots (with fused)
 };
+// Arrival counters of the in-kernel split merge: one per (entry, unit) of a launch.
+constexpr int kDecodeCounters = 16384;
 DecodePlan plan_decode(const DecodeArgs& a);
 // workspace: at least plan.workspace_bytes of device memory (split partials).
 // after_split: when not null, recorded on `stream` between the split kernel
@@ -150,9 +158,11 @@ DecodePlan plan_decode(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, void* workspace, hipStream_t stream,
                          hipEvent_t after_split = nullptr);
 
-// Split partials of the no-allocation decode entry point: a device array of this many
-// bytes (per GPU, for the life of the process).
+// Scratch of the no-allocation decode entry point: a device array of this many bytes (per
+// GPU, for the life of the process), the arrival counters (kDecodeCounterBytes, zero at
+// load) followed by the split partials.
 constexpr size_t kDecodeScratchBytes = size_t(8) << 20;
+constexpr size_t kDecodeCounterBytes = kDecodeCounters * sizeof(unsigned);
 // Device address of that array on `device`, which must be the current device; taken
 // once per device with hipGetSymbolAddress (thread-safe).
 int decode_scratch_address(int device, void** ptr);

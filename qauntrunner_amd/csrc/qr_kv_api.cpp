@@ -24,6 +24,7 @@ struct qr_kv {
     DevBuf stage;      // host <-> device staging of rows, queries and outputs
     DevBuf workspace;  // split-K partials
     DevBuf steppos;    // device positions of the queries of a device-position chunk (kMaxDecodeBatch ints)
+    DevBuf counters;   // arrival counters of the in-kernel split merge (kDecodeCounters, zero between calls)
     hipEvent_t split_event = nullptr;  // benchmark instrumentation (qr_kv_set_split_event)
     void* scratch = nullptr;           // this device's decode scratch array (no-allocation calls)
     bool device_steps = false;         // the device copy of the page accounting is in use
@@ -182,6 +183,7 @@ int decode_dev(qr_kv* kv, int n, const int* seq_ids, const int* seq_len, int lay
             a.seq_len[i] = seq_len[i0 + i];
             a.pt_off[i] = kv->store.pt_offset(seq_ids[i0 + i], layer);
         }
+        a.counters = static_cast<unsigned*>(kv->counters.get());
         const DecodePlan plan = plan_decode(a);
         QR_TRY(grow_workspace(kv, plan.workspace_bytes, stream));
         QR_HIP(launch_decode(a, plan, kv->workspace.get(), stream, kv->split_event));
@@ -265,6 +267,7 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
     }
     if (st == QR_OK) st = decode_scratch_address(kv->device, &kv->scratch);
     if (st == QR_OK) st = kv->steppos.ensure(kMaxDecodeBatch * sizeof(int));
+    if (st == QR_OK) st = kv->counters.ensure(kDecodeCounterBytes, true);
     if (st == QR_OK && hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking) != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed");
         st = QR_ERR_HIP;
@@ -469,14 +472,17 @@ int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer,
     a.out = attn_dev;
     a.scale = scale;
     a.nb = n;
+    // the scratch array holds the arrival counters, then the split partials
+    a.counters = static_cast<unsigned*>(kv->scratch);
     const DecodePlan plan = plan_decode(a);
-    if (plan.workspace_bytes > kDecodeScratchBytes) {
-        set_error("split partials of %zu bytes exceed the %zu-byte scratch of the no-allocation call "
+    if (plan.workspace_bytes > kDecodeScratchBytes - kDecodeCounterBytes) {
+        set_error("split partials of %zu bytes exceed the %zu bytes the no-allocation call's scratch holds "
                   "(fewer entries or shorter sequences per call, or qr_kv_attention_dev)",
-                  plan.workspace_bytes, kDecodeScratchBytes);
+                  plan.workspace_bytes, kDecodeScratchBytes - kDecodeCounterBytes);
         return QR_ERR_OUT_OF_RANGE;
     }
-    QR_HIP(launch_decode(a, plan, kv->scratch, as_stream(stream), kv->split_event));
+    QR_HIP(launch_decode(a, plan, static_cast<char*>(kv->scratch) + kDecodeCounterBytes, as_stream(stream),
+                         kv->split_event));
     return QR_OK;
 }
 
@@ -741,6 +747,7 @@ int rope_step_dev(qr_kv* kv, int seq_id, int layer, int n, const int* pos_dev, f
     for (int i = 0; i < half; ++i) a.freq[i] = std::pow(theta, (-2.0f * static_cast<float>(i)) / static_cast<float>(kv->head_dim));
     QR_HIP(launch_rope_append(a, st));
     kv->store.mark_device_ahead();
+    if (cap) kv->store.mark_replayable();
     return QR_OK;
 }
 
@@ -764,6 +771,7 @@ int attention_step(qr_kv* kv, int n, const int* seq_ids, int layer, const int* p
     a.scale = scale;
     a.nb = n;
     a.pos_dev = pos_dev;
+    a.counters = static_cast<unsigned*>(kv->counters.get());
     const DecodePlan plan = plan_decode(a);
     QR_TRY(grow_workspace(kv, plan.workspace_bytes, st));
     QR_HIP(launch_decode(a, plan, kv->workspace.get(), st, nullptr));

@@ -535,6 +535,7 @@ int qr_mla_append_step_dev(qr_mla* m, int layer, int n, const int* pos0_dev, con
     a.max_seq = m->max_seq;
     QR_HIP(launch_append(a, st));
     m->store.mark_device_ahead();
+    if (cap) m->store.mark_replayable();
     return QR_OK;
 }
 

@@ -77,7 +77,7 @@ int PagedStore::init(const PageGeom& geom, int dtype, int layers, int seqs, int 
 }
 
 int PagedStore::pull(std::vector<int>& seq_len) {
-    if (!device_ahead_) return QR_OK;
+    if (!device_ahead()) return QR_OK;
     QR_HIP(hipDeviceSynchronize());  // the device-side appends were enqueued on caller streams
     QR_HIP(hipMemcpy(state_host_.data(), state_dev_, state_host_.size() * sizeof(int), hipMemcpyDeviceToHost));
     device_ahead_ = false;

@@ -86,7 +86,10 @@ public:
     int held_index(int seq, int layer) const { return 2 + seq * layers_ + layer; }
     int seq_index(int seq) const { return 2 + seqs_ * layers_ + seq; }
     void mark_device_ahead() { device_ahead_ = true; }
-    bool device_ahead() const { return device_ahead_; }
+    // A device-side append captured into a graph may be replayed at any time, so from then on
+    // every host-side call reads the device accounting back first.
+    void mark_replayable() { replayable_ = true; }
+    bool device_ahead() const { return device_ahead_ || replayable_; }
     // Waits for the device, takes pages used and held counts from its copy and stores
     // SeqLen into seq_len; device error bits become an error return (and are cleared).
     int pull(std::vector<int>& seq_len);
@@ -109,6 +112,7 @@ private:
     int* state_dev_ = nullptr;
     std::vector<int> state_host_;
     bool device_ahead_ = false;
+    bool replayable_ = false;
     bool frozen_ = false;
 };
 

@@ -109,14 +109,31 @@ def _f32_dev(t, what, numel=None, multiple=None) -> int:
 
 
 def _weight_dev(w, fmt, rows, cols, what) -> None:
-    """A weight given as a raw torch tensor must be a contiguous GPU buffer holding `rows`
-    rows of `cols` weights in format `fmt` (a Weight or a store view carries its own size)."""
+    """A weight handed to a *_dev call must hold `rows` rows of `cols` weights in format
+    `fmt` before its address reaches a kernel: a Weight is checked against its own format
+    and shape, a store DeviceTensor against its view's format and byte size, a raw torch
+    tensor (a contiguous GPU buffer) against its byte size."""
+    code = format_code(fmt)
+    need = rows * row_bytes(code, cols)
+    if isinstance(w, Weight):
+        if (w.Fmt, w.Rows, w.Cols) != (code, rows, cols):
+            raise ValueError(f"{what}: the Weight is format {w.Fmt} [{w.Rows} x {w.Cols}], "
+                             f"the call reads format {code} [{rows} x {cols}]")
+        return
+    view = getattr(w, "View", None)
+    if view is not None:  # a store DeviceTensor
+        if view.Format != code:
+            raise ValueError(f"{what}: tensor {view.Name} is format {view.Format}, the call reads format {code}")
+        if view.SizeBytes < need:
+            raise ValueError(f"{what}: tensor {view.Name} holds {view.SizeBytes} bytes, {need} needed")
+        return
     if hasattr(w, "is_cuda"):
         if not w.is_cuda or not w.is_contiguous():
             raise ValueError(f"{what}: expected a contiguous tensor on the GPU")
-        need = rows * row_bytes(fmt, cols)
         if w.numel() * w.element_size() < need:
             raise ValueError(f"{what}: {w.numel() * w.element_size()} bytes, {need} needed")
+        return
+    raise ValueError(f"{what}: expected a Weight, a store DeviceTensor or a torch tensor on the GPU")
 
 
 def mla_q_absorb_dev(kvb, fmt, heads, nope, rope, vdim, kv_lora, q, q_tilde, stream=None) -> None:

@@ -207,3 +207,19 @@ def test_device_position_tensors_are_checked_on_the_host():
               _FakeTensor(1, "torch.int32", contiguous=False), None):
         with pytest.raises(ValueError):
             _dev_int32(t, 1, "pos")
+
+
+def test_projection_weights_are_checked_against_the_call():
+    """A store DeviceTensor handed to a *_dev projection must match the call's format and hold
+    the rows it reads; the check runs on the host, before any device address is used."""
+    from qauntrunner_amd.store import DeviceTensor, TensorView
+    from qauntrunner_amd.weights import _weight_dev, row_bytes
+
+    dt = DeviceTensor(TensorView("l0.wq", (8, 256), 4, 8 * row_bytes(4, 256)), 0x1000)  # Q8_0 [8 x 256]
+    _weight_dev(dt, 4, 8, 256, "w")
+    with pytest.raises(ValueError, match="format"):
+        _weight_dev(dt, 6, 8, 256, "w")
+    with pytest.raises(ValueError, match="bytes"):
+        _weight_dev(dt, 4, 16, 256, "w")
+    with pytest.raises(ValueError, match="expected a Weight"):
+        _weight_dev(object(), 4, 8, 256, "w")

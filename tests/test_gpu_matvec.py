@@ -152,6 +152,11 @@ def test_matvec_host_weight_and_errors(gpu):
     got = W.MatVec(x)
     assert_exact(got, np.stack([oracle.matvec(4, raw, 512, x[b]) for b in range(3)]), "host MatVec")
     assert_exact(W.MatVec(x[0]), oracle.matvec(4, raw, 512, x[0]), "host MatVec, one vector")
+    yw = torch.empty((3, 192), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="Weight is format"):
+        qr.matvec_dev(W, 4, 192, 512, dev(x), yw)          # more rows than the Weight holds
+    with pytest.raises(ValueError, match="Weight is format"):
+        qr.matvec_dev(W, 6, 96, 512, dev(x), yw)           # another format
     W.close()
     buf = dev(raw.reshape(-1))
     y = torch.empty((1, 96), dtype=torch.float32, device="cuda")
