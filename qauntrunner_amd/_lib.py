@@ -6,8 +6,11 @@ loaded, every entry point raises.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
+import sys
+import weakref
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # QR_ATTN_LIB selects another build of the same library (the sanitizer builds of the host code)
@@ -169,3 +172,30 @@ def check(status: int) -> None:
     msg = lib.qr_last_error().decode(errors="replace")
     name = lib.qr_status_name(status).decode()
     raise _ERRORS.get(status, QrError)(f"{name}: {msg}")
+
+
+# ---------------------------------------------------------------- handle lifetime
+# Objects that own a library handle (caches, weights, model stores).  They are closed
+# explicitly from an atexit hook, which runs while the HIP runtime is still whole; a
+# finalizer that runs later, during interpreter shutdown, does nothing (the process exit
+# reclaims the memory), so no hipFree or stream destroy reaches a runtime that is already
+# tearing itself down.
+_live = weakref.WeakSet()
+
+
+def track(obj) -> None:
+    """Registers an object with a close() method for the exit-time close."""
+    _live.add(obj)
+
+
+def finalizing() -> bool:
+    return sys.is_finalizing()
+
+
+@atexit.register
+def _close_all() -> None:
+    for obj in list(_live):
+        try:
+            obj.close()
+        except Exception:
+            pass

@@ -107,6 +107,7 @@ class PagedKvCache:
         check(self._lib.qr_kv_create(ctypes.byref(h), layers, heads, kv_heads, head_dim, max_seq,
                                      dtype_code(kv_dtype), max_batch))
         self._h = h
+        _lib.track(self)
         self.Layers, self.Heads, self.KvHeads, self.HeadDim = layers, heads, kv_heads, head_dim
         self.MaxSeq, self.MaxBatch = max_seq, max_batch
         self.KvDtype = dtype_code(kv_dtype)
@@ -119,6 +120,8 @@ class PagedKvCache:
             self._h = None
 
     def __del__(self):
+        if _lib.finalizing():  # the exit hook closed what was open; the runtime may be gone
+            return
         try:
             self.close()
         except Exception:
@@ -365,6 +368,7 @@ class MlaLatentCache:
             check(self._lib.qr_mla_create(ctypes.byref(h), layers, latent_dim - rope, rope, max_seq,
                                           dtype_code(dtype)))
         self._h = h
+        _lib.track(self)
         self.Layers, self.MaxSeq = layers, max_seq
         self.LatentDim = latent_dim
         self.Rope = rope
@@ -386,6 +390,8 @@ class MlaLatentCache:
             self._h = None
 
     def __del__(self):
+        if _lib.finalizing():  # the exit hook closed what was open; the runtime may be gone
+            return
         try:
             self.close()
         except Exception:

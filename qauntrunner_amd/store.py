@@ -64,6 +64,7 @@ class ModelStore:
         h = ctypes.c_void_p()
         check(self._lib.qr_model_open(ctypes.byref(h), path.encode()))
         self._h = h
+        _lib.track(self)
         self.Path = path
         n = ctypes.c_int()
         check(self._lib.qr_model_tensor_count(h, ctypes.byref(n)))
@@ -122,6 +123,8 @@ class ModelStore:
         self.Dispose()
 
     def __del__(self):
+        if _lib.finalizing():  # the exit hook closed what was open; the runtime may be gone
+            return
         try:
             self.Dispose()
         except Exception:

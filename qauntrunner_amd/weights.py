@@ -44,6 +44,7 @@ class Weight:
         check(self._lib.qr_weight_create(ctypes.byref(h), self.Fmt, rows, cols,
                                           raw.ctypes.data_as(ctypes.c_void_p)))
         self._h = h
+        _lib.track(self)
 
     @property
     def handle(self):
@@ -70,6 +71,8 @@ class Weight:
             self._h = None
 
     def __del__(self):
+        if _lib.finalizing():  # the exit hook closed what was open; the runtime may be gone
+            return
         try:
             self.close()
         except Exception:

@@ -222,3 +222,23 @@ def test_dispose_is_idempotent(tmp_path):
     s.Dispose()
     s.Dispose()   # idempotent
     os.remove(path)
+
+
+def test_open_handles_are_closed_at_exit(tmp_path):
+    """A handle still open when the interpreter exits is closed by the library's atexit hook
+    (while the runtime is whole), and finalizers that run during interpreter shutdown do
+    nothing: the process exits with status 0."""
+    import subprocess
+    import sys
+
+    path = str(tmp_path / "exit.qw")
+    qwmodel.write(path, layers=1)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "import qauntrunner_amd as qr\n"
+            "s = qr.ModelStore.Open(%r)\n"
+            "keep = [s]\n"  # still referenced when the interpreter finalizes
+            "print(len(s.Tensors))\n") % (root, path)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert int(r.stdout.strip()) > 0
