@@ -856,7 +856,7 @@ def main():
     ms, wall_ms, kernel_ms, extra = run_gpu(w, args.steps, args.warmup)
     bytes_step, flops_step = algorithmic(w)
     tbs = bytes_step / (ms * 1e-3) / 1e12
-    # The attention call (split-K kernel + merge kernel, as the metric defines it): the
+    # The attention call (split-K kernel + split merge, as the metric defines it): the
     # timed loop is device-bound (host time per step is reported beside it), so the HIP
     # events around the timed steps measure the kernels back to back.
     kms = ms
@@ -881,8 +881,9 @@ def main():
                 "frac": achieved / (HBM_PEAK_TBS * 1e3), "traffic": None}
     roof["traffic"] = profiled_traffic(args.config)
     roof["kernel_us"] = round(kms * 1e3, 3)
-    roof["kernel"] = ("attention call: split-K kernel + merge kernel (HIP events around the timed steps on "
-                      "the launch stream)" if w["kind"] in ("decode", "chunk", "mla") else
+    roof["kernel"] = ("attention call: split-K kernel + split merge (inside the split-K kernel for decode "
+                      "plans whose splits fit one pass of the GPU, else a merge kernel; HIP events around the "
+                      "timed steps on the launch stream)" if w["kind"] in ("decode", "chunk", "mla") else
                       "whole step (HIP events around the timed steps on the launch stream)")
     if kernel_ms:
         roof["split_kernel_us"] = round(kernel_ms * 1e3, 3)

@@ -176,9 +176,10 @@ int qr_kv_attention_dev(qr_kv* kv, int n, const int* seq_ids, int layer, const i
  * hipMalloc).  Same as qr_kv_attention_dev, but the split partials live in a
  * fixed 8 MiB device array of the library (one per GPU, held until the process
  * ends) instead of the handle's workspace, which grows with hipMalloc; nothing is
- * allocated, on the host or the device.  At most 64 entries per call; a call whose
- * split partials (entries x heads x splits x (head_dim x 4 + 8) bytes) exceed
- * 8 MiB returns QR_ERR_OUT_OF_RANGE.  Every call on a GPU shares that GPU's array,
+ * allocated, on the host or the device.  The array's first 64 KiB hold the split
+ * merge's arrival counters (zero between calls), the rest the partials.  At most 64
+ * entries per call; a call whose split partials (entries x heads x splits x
+ * (head_dim x 4 + 8) bytes) exceed 8 MiB - 64 KiB returns QR_ERR_OUT_OF_RANGE.  Every call on a GPU shares that GPU's array,
  * whatever the handle: calls that overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller. */
 int qr_kv_attention_dev_noalloc(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos,
@@ -208,13 +209,16 @@ int qr_kv_attention_chunk_step_dev(qr_kv* kv, int seq_id, int layer, int nq, con
 /* Benchmark instrumentation, no reference counterpart: when `event` (a
  * hipEvent_t) is not NULL, every later attention call records it on its
  * stream right after the split-K kernel and before the combine kernel, so a
- * caller can time the split-K kernel alone.  NULL turns it off. */
+ * caller can time the split-K kernel alone (a decode split-K kernel that merges
+ * its own splits launches no combine kernel).  NULL turns it off. */
 int qr_kv_set_split_event(qr_kv* kv, void* event);
 
 /* Introspection, no reference counterpart: the split-K plan a decode call with
  * these entries would take (as qr_kv_attention_batch / _dev, first 64 entries):
  * tokens per split (a multiple of 256) and the number of splits of the longest
- * entry (1: the split kernel writes the output, no merge).  Validates like the
+ * entry (1: the split kernel writes the output, no merge; more: the last split of
+ * each kv head to finish merges them inside the split kernel when all splits run
+ * in one pass of the GPU, else a merge kernel follows).  Validates like the
  * attention call; launches nothing. */
 int qr_kv_decode_plan(qr_kv* kv, int n, const int* seq_ids, int layer, const int* pos, int* split_tokens,
                       int* splits);

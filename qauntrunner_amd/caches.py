@@ -271,7 +271,7 @@ class PagedKvCache:
 
     def AttentionDevNoAlloc(self, layer, seq_ids, positions, q, out, scale, stream=None) -> None:
         """AttentionDev through qr_kv_attention_dev_noalloc: split partials in the library's
-        fixed device array, no allocation (at most 64 entries, 8 MiB of partials)."""
+        fixed device array, no allocation (at most 64 entries, 8 MiB - 64 KiB of partials)."""
         ids = np.ascontiguousarray(seq_ids, dtype=np.int32)
         pos = np.ascontiguousarray(positions, dtype=np.int32)
         if pos.size != ids.size:

@@ -49,7 +49,7 @@ def test_noalloc_decode_matches_the_allocating_call(gpu, dtype):
 
 
 def test_noalloc_decode_rejects_partials_beyond_its_array(gpu):
-    """64 entries x 128 heads x 2 splits x 520 bytes = 8.5 MB > 8 MiB: rejected."""
+    """64 entries x 128 heads x 2 splits x 520 bytes = 8.5 MB > 8 MiB - 64 KiB: rejected."""
     import torch
 
     heads, kv_heads, D, n = 128, 1, 128, 8192
