@@ -176,9 +176,17 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     const int vdim = lane >> 3;                          // dim row inside a V instruction
     const int vslot = lane & 7;
     const int vchunk = vslot ^ ((vdim >> 1) & 3) ^ ((wave & 1) << 2);  // n & 1 == wave & 1
-    auto dma = [&](int it) {
+    // Page-table entry of tile `it`: a scalar load through the constant address space (no
+    // kernel writes the table while this one runs), fetched one tile before its DMA is
+    // issued.  As a vector load it needed a vmcnt(0) before its readfirstlane, which
+    // drained the tile DMA still in flight on every iteration.
+    auto page_entry = [&](int it) {
+        return reinterpret_cast<const __attribute__((address_space(4))) int*>(
+            reinterpret_cast<uintptr_t>(p.page_table))[(t_begin + it * kTile) >> kPageShift];
+    };
+    auto dma = [&](int it, int phys_entry) {
         const int t0 = t_begin + it * kTile;
-        const long long phys = p.page_table[t0 >> kPageShift];
+        const long long phys = phys_entry;
         const int slot0 = t0 & (kPageTokens - 1);
         const int nvalid = min(kTile, t_end - t0);
         char* dst = lds[it % NSTAGE];
@@ -211,8 +219,9 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     // so that fp16 cannot overflow; log2-unit score scale per row
     vec8 qhi[NT][NK], qlo[NT][NK];
     float sscale[NT];
-    if (ntiles > 0) dma(0);
-    if (NSTAGE > 2 && ntiles > 1) dma(1);
+    if (ntiles > 0) dma(0, page_entry(0));
+    if (NSTAGE > 2 && ntiles > 1) dma(1, page_entry(1));
+    int phys_pf = NSTAGE - 1 < ntiles ? page_entry(NSTAGE - 1) : 0;  // the next DMA's page
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const size_t qrow = (static_cast<size_t>(row_on[j] ? row_q[j] : 0) * p.heads + row_h[j]) * D;
@@ -265,7 +274,10 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         if (NSTAGE > 2 && it + 1 < ntiles) wait_vmcnt<PER_TILE>();
         else wait_dma();
         lds_barrier();
-        if (it + NSTAGE - 1 < ntiles) dma(it + NSTAGE - 1);
+        if (it + NSTAGE - 1 < ntiles) {
+            dma(it + NSTAGE - 1, phys_pf);
+            if (it + NSTAGE < ntiles) phys_pf = page_entry(it + NSTAGE);
+        }
         const char* kt = lds[it % NSTAGE];
         const char* vt = kt + KB;
         const int nvalid = min(kTile, t_end - t0);
