@@ -104,6 +104,28 @@ __device__ __forceinline__ int chunk_split_tokens(const ChunkK& p, int pos0) {
     return (tiles + p.splits - 1) / p.splits * kTile;
 }
 
+// Row maxima of the scores in v_max3_f32 / v_max_f32.  The scores come straight from the
+// MFMAs, so the quieting of signalling NaNs that fmaxf implies (one extra v_max per
+// operand, half the VALU of the max) is not needed: a NaN score still reaches its row's
+// output through P.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max2f(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// max over the four lane quarters of a row (lanes l ^ 16, l ^ 32)
+__device__ __forceinline__ float max_quarters(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // BF16: cache element type; NT: 16-row N tiles per wave; NSTAGE: LDS tile buffers;
 // QSPLIT: q is not exact in the cache type and enters as hi + lo parts.
 template <bool BF16, int D, int NT, int NSTAGE, bool QSPLIT>
@@ -336,12 +358,14 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         bool any_rescale = false;
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                tmax = fmaxf(tmax, fmaxf(fmaxf(sc[j][mt][0], sc[j][mt][1]), fmaxf(sc[j][mt][2], sc[j][mt][3])));
-            tmax = max_xor16(tmax);
-            tmax = max_xor32(tmax);
+            // the lane's 16 scores: five v_max3 over 15 of them, two more over those five
+            // and the last, one v_max; then the other lane quarters
+            const float a0 = max3f(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
+            const float a1 = max3f(sc[j][0][3], sc[j][1][0], sc[j][1][1]);
+            const float a2 = max3f(sc[j][1][2], sc[j][1][3], sc[j][2][0]);
+            const float a3 = max3f(sc[j][2][1], sc[j][2][2], sc[j][2][3]);
+            const float a4 = max3f(sc[j][3][0], sc[j][3][1], sc[j][3][2]);
+            const float tmax = max_quarters(max2f(max3f(a0, a1, a2), max3f(a3, a4, sc[j][3][3])));
             ts[j] = tmax * sscale[j];
             grow[j] = ts[j] > m[j] + 8.f;
             any_rescale |= grow[j] && m[j] != -INFINITY;
