@@ -321,17 +321,29 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) sc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // The K operands of M tile mt+1 are read before the MFMAs of M tile mt (scheduling
+        // barriers keep the compiler from sinking each read next to its first use, where
+        // every MFMA pair waited out an LDS round trip).
+        {
+            vec8 ka[2][NK];
+            auto kread = [&](int mt, vec8 (&dst)[NK]) __attribute__((always_inline)) {
+                const char* row = kt + kq_off + (32 * (mt >> 1) + 4 * (mt & 1)) * RB;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const char* row = kt + kq_off + (32 * (mt >> 1) + 4 * (mt & 1)) * RB;
+                for (int kk = 0; kk < NK; ++kk) dst[kk] = *reinterpret_cast<const vec8*>(row + 16 * ((4 * kk + q4) ^ kq_swz));
+            };
+            kread(0, ka[0]);
 #pragma unroll
-            for (int kk = 0; kk < NK; ++kk) {
-                const vec8 a = *reinterpret_cast<const vec8*>(row + 16 * ((4 * kk + q4) ^ kq_swz));
+            for (int mt = 0; mt < 4; ++mt) {
+                if (mt + 1 < 4) kread(mt + 1, ka[(mt + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    sc[j][mt] = mfma16(a, qhi[j][kk], sc[j][mt]);
-                    if (QSPLIT) sc[j][mt] = mfma16(a, qlo[j][kk], sc[j][mt]);
-                }
+                for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        sc[j][mt] = mfma16(ka[mt & 1][kk], qhi[j][kk], sc[j][mt]);
+                        if (QSPLIT) sc[j][mt] = mfma16(ka[mt & 1][kk], qlo[j][kk], sc[j][mt]);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
 
@@ -391,17 +403,22 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
                     pb[j][mt >> 1][4 * (mt & 1) + r] = static_cast<T>(fast_exp2(fmaf(sc[j][mt][r], sscale[j], mneg)));
         }
 
-        // ---- PV (and the row sums: a ones operand turns the MFMA into sum over positions)
+        // ---- PV (and the row sums: a ones operand turns the MFMA into sum over positions).
+        // Every V^T operand of a k-slot half is read before its MFMAs (a scheduling barrier
+        // keeps the reads ahead), so the later reads land while the first MFMAs run.
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+            vec8 va[NDT];
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                va[dt] = *reinterpret_cast<const vec8*>(vt + (16 * dt + col) * 128 + 16 * ((4 * ks + q4) ^ pv_swz));
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < NT; ++j) accl[j] = mfma16(ones, pb[j][ks], accl[j]);
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const vec8 a = *reinterpret_cast<const vec8*>(vt + (16 * dt + col) * 128 + 16 * ((4 * ks + q4) ^ pv_swz));
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                for (int j = 0; j < NT; ++j) acc[j][dt] = mfma16(a, pb[j][ks], acc[j][dt]);
-            }
+                for (int j = 0; j < NT; ++j) acc[j][dt] = mfma16(va[dt], pb[j][ks], acc[j][dt]);
         }
     }
 
