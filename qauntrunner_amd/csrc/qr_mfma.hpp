@@ -51,16 +51,18 @@ __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
 constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 constexpr int kCacheSc1 = 16;             // buffer intrinsic cache-policy bits: sc1 (device scope)
+constexpr int kCacheNt = 2;               // buffer intrinsic cache-policy bits: nt (streamed, read once)
 
 // 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
 // ... lds); out-of-range offsets read zeros.  `lds` must be the same for every lane of
 // the wave (it becomes M0, which the compiler sets).  The compiler does not track when
 // an LDS DMA lands, so completion is awaited explicitly (wait_vmcnt, then a barrier when
 // other waves read the data) before the data is read.
+template <int AUX = 0>
 __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, const char* lds, uint32_t voffset,
                                                   uint32_t soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (__attribute__((address_space(3))) void*)(const_cast<char*>(lds)), 16, voffset, soffset, 0, 0);
+        rsrc, (__attribute__((address_space(3))) void*)(const_cast<char*>(lds)), 16, voffset, soffset, 0, AUX);
 }
 
 }  // namespace qr
