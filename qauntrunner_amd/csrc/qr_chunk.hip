@@ -85,6 +85,7 @@ struct ChunkK {
     int qblocks;
     int units;               // splits x qblocks x kv_heads
     int per_xcd;             // launch slots per XCD: ceil(units / 8)
+    int kv_once;             // one query block: each K/V line is read once per call
 };
 
 // Position of query 0: the argument, or the device-side one bounded by it (a scalar load:
@@ -227,13 +228,15 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
                 r = 8 * n + (lane >> 3);
                 c = (lane & 7) ^ (((r >> 1) & 1) | ((r >> 2) & 6));
             }
-            buffer_load_lds16(rk, dst + 1024 * n, r * RB + 16 * c, 0);
+            if (p.kv_once) buffer_load_lds16<kCacheNt>(rk, dst + 1024 * n, r * RB + 16 * c, 0);
+            else buffer_load_lds16(rk, dst + 1024 * n, r * RB + 16 * c, 0);
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             const int n = wave + 4 * i;                      // dims 8n .. 8n+7
             const uint32_t off = (vdim * kPageTokens * 2 + 16 * vchunk) + (8 * vchunk >= nvalid ? 0x40000000u : 0u);
-            buffer_load_lds16(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
+            if (p.kv_once) buffer_load_lds16<kCacheNt>(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
+            else buffer_load_lds16(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
         }
     };
 
@@ -572,6 +575,11 @@ hipError_t launch_chunk(const ChunkArgs& a, const ChunkPlan& pl, void* workspace
     k.qblocks = pl.qblocks;
     k.units = pl.splits * pl.qblocks * a.geom.kv_heads;
     k.per_xcd = (k.units + 7) / 8;
+    // With one query block per kv head every K/V line is read once per call and the loads
+    // are marked non-temporal (C4 verify: 101.7-102.2 vs 104.1-104.2 us in one A/B run, no
+    // difference in another); query blocks that share a kv head re-read its tiles through
+    // L2 and keep the default policy (C3 232.8 with nt vs 230.5 us).
+    k.kv_once = pl.qblocks == 1;
     const dim3 grid(8 * k.per_xcd);
     const bool bf = a.kv_dtype == QR_DTYPE_BF16;
     const bool qsplit = a.q_dtype != a.kv_dtype;  // q not exact in the cache's 16-bit type
