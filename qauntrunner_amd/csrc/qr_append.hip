@@ -94,11 +94,12 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherArgs a) {
 constexpr int kRopeRows = 1;
 constexpr int kVTileTpt = 8;       // V tile: tokens per thread (one 16-byte chunk per dim)
 
-// 4 consecutive dims of one cache row: one 16- or 8-byte store when the plane is
-// token-major, element stores when it is dims-major.
+// 4 consecutive dims of one cache row (d a multiple of 4): one 16- or 8-byte store when
+// they are contiguous (token-major planes and MFMA-layout K), element stores for an
+// MFMA-layout V plane.
 __device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g, long long phys, int plane, int kvh,
                                        int slot, int d, const float (&x)[4]) {
-    const bool rows = !(plane == 1 && g.v_dims_major);
+    const bool rows = !(plane == 1 && g.mfma_layout);
     if (dtype == QR_DTYPE_F32 && rows) {
         *reinterpret_cast<float4*>(static_cast<float*>(pool) + g.offset(phys, plane, kvh, slot, d)) =
             make_float4(x[0], x[1], x[2], x[3]);
@@ -117,8 +118,8 @@ __device__ __forceinline__ void store4(void* pool, int dtype, const PageGeom& g,
     for (int e = 0; e < 4; ++e) base[g.offset(phys, plane, kvh, slot, d + e)] = b[e];
 }
 
-// A dims-major V plane keeps one dim of kPageTokens tokens contiguous, so a position's V
-// row lands as 2-byte stores 2*kPageTokens bytes apart.  V tiles write it instead: a
+// An MFMA-layout V plane keeps 8 aligned consecutive tokens of one dim contiguous, so a
+// position's V row lands as scattered 2-byte stores.  V tiles write it instead: a
 // workgroup owns an aligned run of T tokens of one kv head (T divides kPageTokens, so
 // the run lies in one page), each thread 2 dims x TPT consecutive tokens, and a chunk of
 // 8 tokens of one dim is one 16-byte store.  Source rows outside [pos0, pos0 + n) are
@@ -128,7 +129,7 @@ __host__ __device__ constexpr int v_tile_tokens(int head_dim, int tpt) { return 
 
 template <int TPT>
 __device__ __forceinline__ void v_tile_store(const AppendArgs& g, int pos0, int vb) {
-    static_assert(TPT % 8 == 0, "whole 16-byte chunks");
+    static_assert(TPT == 8, "one 16-byte chunk (8 aligned tokens of one dim) per thread and dim");
     const int D = g.geom.head_dim;
     const int pairs = D >> 1;  // 32 or 64
     const int T = v_tile_tokens(D, TPT);
@@ -374,8 +375,8 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     const int D = a.app.geom.head_dim;
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
     const int ipt = rope_items_per_thread(heads, D);
-    // V tiles: 16-bit dims-major V plane (head_dim 64 or 128), kVTileTpt tokens per thread
-    const bool tiles = a.app.geom.v_dims_major && a.app.geom.planes == 2 && (D == 64 || D == 128) &&
+    // V tiles: 16-bit MFMA-layout V plane (head_dim 64 or 128), kVTileTpt tokens per thread
+    const bool tiles = a.app.geom.mfma_layout && a.app.geom.planes == 2 && (D == 64 || D == 128) &&
                        a.app.dtype != QR_DTYPE_F32;
     int nv = 0;
     if (tiles) {

@@ -11,11 +11,13 @@
 // wave owns its rows for the whole split, so waves never exchange data inside a tile.
 //   QK: S^T[pos][row] = K[pos][dims] . Q^T[dims][row]     (M positions, N rows)
 //   PV: O^T[dim][row] += V^T[dim][pos] . P^T[pos][row]     (M dims,      N rows)
-// Tiles of 64 positions are copied into LDS by buffer-load DMA (K row-major, V^T
-// straight from the dims-major V block of the page), NSTAGE-buffered, with XOR
-// swizzles that keep the 16 rows of every MFMA operand read on distinct banks.  QK
-// row m of M tile mt is position 32(mt/2) + 8(m/4) + 4(mt%2) + m%4, so after QK lane
-// quarter q holds the scores of positions 32ks + 8q .. +7, its PV k-slots of step ks.
+// Tiles of 64 positions -- two steps of the MFMA operand page layout (qr_kernels.hpp) --
+// are copied into LDS by buffer-load DMA as they lie in the page, NSTAGE-buffered, so
+// every MFMA operand is a contiguous 1 KiB of LDS that a wave reads conflict-free, 16
+// bytes per lane, and every DMA wave load covers whole 128-byte lines.  QK row m of M
+// tile mt is position 32(mt/2) + 8(m/4) + 4(mt%2) + m%4 (the page layout's K operand
+// order), so after QK lane quarter q holds the scores of positions 32ks + 8q .. +7, its
+// PV k-slots of step ks.
 // Operands stay in the cache's 16-bit type (no conversion); q enters as hi + lo parts
 // when its own type is not the cache's (fp32 queries keep ~22 or ~16 bits), P is
 // rounded to the cache type; accumulation and softmax are fp32.  Row sums come from
@@ -190,15 +192,12 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     const int ntiles = t_end > t_begin ? (t_end - t_begin + kTile - 1) / kTile : 0;
     const int unmasked_end = pos0 + q_first + 1;  // positions below it are seen by every row
 
-    // ---- DMA of tile `it` into stage it % NSTAGE.  K: row t of the tile at t*RB, its
-    // chunk c at slot c ^ fk(t); V^T: dim row d at KB + 128 d, chunk c (positions
-    // 8c..8c+7) at slot c ^ ((d >> 1) & 7).  Rows past the end read zeros (K: buffer
-    // range; V: chunks wholly past the end are sent out of range, the one partial
-    // chunk per row is cleared after it lands).
+    // ---- DMA of tile `it` into stage it % NSTAGE: the tile's two steps of K, then of V,
+    // contiguous in the page, copied as they lie (1 KiB per wave load).  Positions past
+    // the end are masked out of the scores (K) or cleared after they land (V, last tile
+    // only), so a zero weight never meets a stale row.
     const long long kblk = static_cast<long long>(kvh) * kPageTokens * D;
-    const int vdim = lane >> 3;                          // dim row inside a V instruction
-    const int vslot = lane & 7;
-    const int vchunk = vslot ^ ((vdim >> 1) & 3) ^ ((wave & 1) << 2);  // n & 1 == wave & 1
+    const uint32_t lane16 = static_cast<uint32_t>(16 * lane);
     // Page-table entry of tile `it`: a scalar load through the constant address space (no
     // kernel writes the table while this one runs), fetched one tile before its DMA is
     // issued.  As a vector load it needed a vmcnt(0) before its readfirstlane, which
@@ -211,32 +210,22 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         const int t0 = t_begin + it * kTile;
         const long long phys = phys_entry;
         const int slot0 = t0 & (kPageTokens - 1);
-        const int nvalid = min(kTile, t_end - t0);
         char* dst = lds[it % NSTAGE];
         const char* kbase = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
-        const char* vbase = p.pool + (phys * p.page_elems + p.plane_elems + kblk + slot0) * 2;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, nvalid * RB, kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vbase), 0, (D - 1) * kPageTokens * 2 + kTile * 2, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kbase), 0, KB, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(kbase + p.plane_elems * 2), 0, VB, kBufferFlags);
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int n = wave + 4 * i;
-            int r, c;
-            if (D == 128) {  // 4 rows per instruction, 16 chunks per row; fk(t) = t0 t1 t3 t4
-                r = 4 * n + (lane >> 4);
-                c = (lane & 15) ^ ((r & 3) | ((r >> 1) & 12));
-            } else {         // 8 rows per instruction, 8 chunks per row; fk(t) = t1 t3 t4
-                r = 8 * n + (lane >> 3);
-                c = (lane & 7) ^ (((r >> 1) & 1) | ((r >> 2) & 6));
-            }
-            if (p.kv_once) buffer_load_lds16<kCacheNt>(rk, dst + 1024 * n, r * RB + 16 * c, 0);
-            else buffer_load_lds16(rk, dst + 1024 * n, r * RB + 16 * c, 0);
+            if (p.kv_once) buffer_load_lds16<kCacheNt>(rk, dst + 1024 * n, lane16, 1024 * n);
+            else buffer_load_lds16(rk, dst + 1024 * n, lane16, 1024 * n);
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int n = wave + 4 * i;                      // dims 8n .. 8n+7
-            const uint32_t off = (vdim * kPageTokens * 2 + 16 * vchunk) + (8 * vchunk >= nvalid ? 0x40000000u : 0u);
-            if (p.kv_once) buffer_load_lds16<kCacheNt>(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
-            else buffer_load_lds16(rv, dst + KB + 1024 * n, off, 8 * n * kPageTokens * 2);
+            const int n = wave + 4 * i;
+            if (p.kv_once) buffer_load_lds16<kCacheNt>(rv, dst + KB + 1024 * n, lane16, 1024 * n);
+            else buffer_load_lds16(rv, dst + KB + 1024 * n, lane16, 1024 * n);
         }
     };
 
@@ -287,10 +276,10 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         for (int t = 0; t < NDT; ++t) acc[j][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     // QK row m of M tile mt is position 32(mt/2) + 8(m/4) + 4(mt%2) + m%4, so lane quarter
-    // q4 ends with positions 32ks + 8q4 .. +7: its PV k-slots of step ks in order.
-    const int kq_off = (32 * 0 + 8 * (col >> 2) + (col & 3)) * RB;  // + (32(mt/2) + 4(mt%2)) * RB
-    const int kq_swz = D == 128 ? col : ((col >> 1) & 7);           // fk of every row this lane reads
-    const int pv_swz = (col >> 1) & 7;                              // V^T slot swizzle of dim row 16dt + col
+    // q4 ends with positions 32ks + 8q4 .. +7: its PV k-slots of step ks in order.  In LDS
+    // a step is SB bytes: K operand (mt % 2, kk) at 1024 ((mt % 2) NK + kk), V operand dt
+    // at 1024 dt, lane L's 16 bytes at 16 L.
+    constexpr int SB = 64 * D;
 
     for (int it = 0; it < ntiles; ++it) {
         const int t0 = t_begin + it * kTile;
@@ -306,14 +295,17 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         const char* kt = lds[it % NSTAGE];
         const char* vt = kt + KB;
         const int nvalid = min(kTile, t_end - t0);
-        if (nvalid & 7) {
-            // the partial V chunk of every dim row: clear positions past the end
-            const int cp = nvalid >> 3;
-            for (int d = threadIdx.x; d < D; d += 256) {
-                uint32_t* w = reinterpret_cast<uint32_t*>(const_cast<char*>(vt) + d * 128 + 16 * (cp ^ ((d >> 1) & 7)));
+        if (nvalid < kTile) {
+            // the last tile: clear V past the end.  16-byte chunk c of the V tile (step
+            // c / (NDT 64), dim tile, lane L = c % 64) holds positions 32 step + 8 (L / 16)
+            // .. + 7 of one dim.
+            for (int c = threadIdx.x; c < 2 * NDT * 64; c += 256) {
+                const int pb = 32 * (c / (NDT * 64)) + 8 * ((c & 63) >> 4);
+                if (pb + 8 <= nvalid) continue;
+                uint32_t* w = reinterpret_cast<uint32_t*>(const_cast<char*>(vt) + 16 * c);
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
-                    if (8 * cp + i >= nvalid) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                    if (pb + i >= nvalid) w[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
             }
             lds_barrier();
         }
@@ -330,9 +322,9 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
         {
             vec8 ka[2][NK];
             auto kread = [&](int mt, vec8 (&dst)[NK]) __attribute__((always_inline)) {
-                const char* row = kt + kq_off + (32 * (mt >> 1) + 4 * (mt & 1)) * RB;
+                const char* op = kt + SB * (mt >> 1) + 1024 * NK * (mt & 1) + 16 * lane;
 #pragma unroll
-                for (int kk = 0; kk < NK; ++kk) dst[kk] = *reinterpret_cast<const vec8*>(row + 16 * ((4 * kk + q4) ^ kq_swz));
+                for (int kk = 0; kk < NK; ++kk) dst[kk] = *reinterpret_cast<const vec8*>(op + 1024 * kk);
             };
             kread(0, ka[0]);
 #pragma unroll
@@ -414,7 +406,7 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
             vec8 va[NDT];
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
-                va[dt] = *reinterpret_cast<const vec8*>(vt + (16 * dt + col) * 128 + 16 * ((4 * ks + q4) ^ pv_swz));
+                va[dt] = *reinterpret_cast<const vec8*>(vt + SB * ks + 1024 * dt + 16 * lane);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < NT; ++j) accl[j] = mfma16(ones, pb[j][ks], accl[j]);

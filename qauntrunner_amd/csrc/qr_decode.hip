@@ -551,15 +551,19 @@ streamed:
 }
 
 // ---------------------------------------------------------------------------
-// MFMA decode for 16-bit caches with head_dim 64 or 128 (V stored dims-major).
+// MFMA decode for 16-bit caches with head_dim 64 or 128 (pages in the MFMA operand layout).
 //
 // Workgroup = 4 waves, one unit (a kv head and up to 16 of its query heads), one
 // split.  The split is walked in 32-position steps; wave w takes steps w, w+4, ...
 // with its own online softmax, and the four waves are merged through LDS at the end.
-//   QK  S^T[pos][head] = K[pos][dims] . q^T[dims][head]: A = 16 K rows loaded straight
-//       from the page (16 bytes per lane and k-step), B = q held in registers.
+//   QK  S^T[pos][head] = K[pos][dims] . q^T[dims][head]: A = 16 K rows, one 1 KiB
+//       operand block of the page (16 bytes per lane), B = q held in registers.
 //   PV  O^T[dim][head] += V^T[dim][pos] . P^T[pos][head]: A = 8 consecutive positions
-//       of one dim, a single 16-byte load from the dims-major V block.
+//       of each of 16 dims, one 1 KiB operand block of the V plane.
+// Each wave load reads whole 128-byte lines and is marked non-temporal (with the
+// earlier token-major K and dims-major V each load read half lines, the other halves
+// by the next k-step or another wave's step, and nt loads then lost the lines between
+// the two; C2 fp16 B1 / C4 decode / fp16 B16 measured 32.6 / 98.4 / 360 us then).
 // v_mfma_f32_16x16x32_{f16,bf16} lane layout (checked on gfx950):
 //   A[m = lane%16][k = 8*(lane/16)+i], B[k = 8*(lane/16)+i][n = lane%16],
 //   D[m = 4*(lane/16)+r][n = lane%16].
@@ -613,7 +617,6 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     }
     const int* pt = p.page_table + p.pt_off[b];
     const long long kblk = static_cast<long long>(kvh) * kPageTokens * D;
-    const int krow = 8 * (n >> 2) + (n & 3);  // QK row of this lane in M tile 0 (+4 in tile 1)
     const int total_steps = (t_end - t_begin + kStep - 1) / kStep;
     const int nst = total_steps > wave ? (total_steps - wave + kWaves - 1) / kWaves : 0;
     // splits start at different steps and wrap around (see decode_stream_kernel)
@@ -629,29 +632,27 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
             reinterpret_cast<uintptr_t>(pt))[__builtin_amdgcn_readfirstlane(step_t0(st)) >> kPageShift];
     };
     // Loads of step st into buffer buf: buffer loads from a wave-uniform base (the step's
-    // first K row and its V^T column block, in SGPRs) plus loop-invariant lane offsets, so
-    // no per-step vector address is built (a per-step address in registers that the
+    // K and V operand blocks, in SGPRs) plus the loop-invariant lane offset, so no
+    // per-step vector address is built (a per-step address in registers that the
     // previous step's loads were still writing made the compiler drain every load in
-    // flight at the loop head).
-    const uint32_t k_lane = static_cast<uint32_t>((krow * D + 8 * q4) * 2);
-    const uint32_t v_lane = static_cast<uint32_t>((n * kPageTokens + 8 * q4) * 2);
+    // flight at the loop head).  A step is 32 x D contiguous elements of each plane.
+    const uint32_t lane16 = static_cast<uint32_t>(16 * lane);
     auto issue_at = [&](int st, long long phys, int buf) {
         const int t0 = __builtin_amdgcn_readfirstlane(step_t0(st));  // a step never crosses a page
         const int slot0 = t0 & (kPageTokens - 1);
         const char* kp = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
-        const char* vp = p.pool + (phys * p.page_elems + p.plane_elems + kblk + slot0) * 2;
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kp), 0, 0x7FFFFFFF, kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vp), 0, 0x7FFFFFFF, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(kp + p.plane_elems * 2), 0, 0x7FFFFFFF, kBufferFlags);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int kk = 0; kk < NK; ++kk)
                 kb[buf][mt][kk] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                    rk, k_lane + static_cast<uint32_t>((4 * mt * D + 32 * kk) * 2), 0, 0));
+                    rk, lane16, 1024 * (mt * NK + kk), kCacheNt));
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-            vb[buf][dt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                rv, v_lane, static_cast<uint32_t>(16 * dt * kPageTokens * 2), 0));
+            vb[buf][dt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane16, 1024 * dt, kCacheNt));
     };
     if (nst > 0) issue_at(wave, phys_of(wave), 0);
 
@@ -985,8 +986,8 @@ int cu_count() {
     return cus;
 }
 
-// The dims-major V layout marks the caches whose decode runs on MFMA tiles.
-bool uses_mfma(const DecodeArgs& a) { return a.geom.v_dims_major != 0; }
+// The MFMA operand page layout marks the caches whose decode runs on MFMA tiles.
+bool uses_mfma(const DecodeArgs& a) { return a.geom.mfma_layout != 0; }
 
 int units_of(const DecodeArgs& a, int* gmax) {
     const int kvh = a.geom.kv_heads;

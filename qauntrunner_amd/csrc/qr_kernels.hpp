@@ -10,26 +10,51 @@ namespace qr {
 //   page = planes x kv_heads x kPageTokens x head_dim
 // plane 0 holds K, plane 1 holds V (GQA cache); the MLA cache has one plane with
 // kv_heads = 1 and head_dim = latent width.  Inside a plane each kv head owns a
-// contiguous block of kPageTokens x head_dim elements: [token][dim] (one
-// contiguous stream of 256 rows), or, for the V plane when v_dims_major is set,
-// [dim][token], so that the 16-bit MFMA kernels read V^T operands (8 consecutive
-// tokens of one dim) as single 16-byte loads.
+// contiguous block of kPageTokens x head_dim elements: [token][dim] (one contiguous
+// stream of 256 rows), or, when mfma_layout is set (16-bit caches with head_dim 64 or
+// 128), the MFMA operand layout below.
+//
+// MFMA operand layout: the block is 8 steps of 32 tokens, step s holding tokens
+// 32s..32s+31 in 32 x head_dim contiguous elements, cut into 1 KiB operand blocks of
+// 64 x 8 elements; element e of lane L sits at 512 b + 8 L + e.  Lane L = 16 q + n is
+// the lane that holds those 8 elements as an operand of v_mfma_f32_16x16x32_{f16,bf16}
+// (A[m = n][k = 8 q + e]):
+//   K (plane 0): block b = mt * head_dim/32 + kk holds token 8 (n / 4) + 4 mt + n % 4
+//                of the step, dims 32 kk + 8 q + e (the QK A operand of M tile mt,
+//                k-step kk);
+//   V (plane 1): block b = dt holds dim 16 dt + n, tokens 8 q + e of the step (the PV
+//                A operand of dim tile dt).
+// So every operand the decode and chunk kernels feed to an MFMA is one contiguous
+// 1 KiB (whole 128-byte lines per wave load, which the loads can mark non-temporal),
+// and 8 consecutive dims of a K row or 8 aligned consecutive tokens of one V dim are one
+// contiguous 16-byte run for the appends.
 struct PageGeom {
     int planes;
     int kv_heads;
     int head_dim;
-    int v_dims_major = 0;
+    int mfma_layout = 0;
     __host__ __device__ long long plane_elems() const { return (long long)kv_heads * kPageTokens * head_dim; }
     __host__ __device__ long long page_elems() const { return plane_elems() * planes; }
     // element offset of (plane, kv head, slot, dim) inside page `phys`
     __host__ __device__ long long offset(long long phys, int plane, int kvh, int slot, int d) const {
         const long long blk = phys * page_elems() + plane * plane_elems() + (long long)kvh * kPageTokens * head_dim;
-        return plane == 1 && v_dims_major ? blk + (long long)d * kPageTokens + slot : blk + (long long)slot * head_dim + d;
+        if (!mfma_layout) return blk + (long long)slot * head_dim + d;
+        const int r = slot & 31;  // token within its step
+        int b, lane;
+        if (plane == 0) {
+            b = ((r >> 2) & 1) * (head_dim >> 5) + (d >> 5);
+            lane = 16 * ((d >> 3) & 3) + (((r >> 3) << 2) | (r & 3));
+        } else {
+            b = d >> 4;
+            lane = 16 * (r >> 3) + (d & 15);
+        }
+        const int e = plane == 0 ? (d & 7) : (r & 7);
+        return blk + (long long)(slot >> 5) * 32 * head_dim + 512 * b + 8 * lane + e;
     }
 };
-// 16-bit GQA caches with head_dim 64 or 128 keep V dims-major (their decode and
-// chunk kernels run on MFMA tiles).
-inline bool kv_v_dims_major(int dtype, int head_dim) {
+// 16-bit GQA caches with head_dim 64 or 128 use the MFMA operand layout (their decode
+// and chunk kernels run on MFMA tiles).
+inline bool kv_mfma_layout(int dtype, int head_dim) {
     return dtype != QR_DTYPE_F32 && (head_dim == 64 || head_dim == 128);
 }
 

@@ -262,7 +262,7 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
     }
     if (st == QR_OK) {
         PageGeom g{2, kv_heads, head_dim};
-        g.v_dims_major = kv_v_dims_major(kv_dtype, head_dim) ? 1 : 0;
+        g.mfma_layout = kv_mfma_layout(kv_dtype, head_dim) ? 1 : 0;
         st = kv->store.init(g, kv_dtype, layers, max_batch, max_seq);
     }
     if (st == QR_OK) st = decode_scratch_address(kv->device, &kv->scratch);
