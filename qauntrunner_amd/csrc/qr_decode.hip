@@ -333,7 +333,10 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
             reinterpret_cast<uintptr_t>(pt))[__builtin_amdgcn_readfirstlane(t0_in) >> kPageShift];
     };
     // t0: first row of the step (wave-uniform: a step never crosses a page); phys: its page
-    auto issue_at = [&](int t0_in, long long phys, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC]) {
+    // live = false: a step past the end, issued only to keep the load count of every
+    // iteration the same; its buffer resource has no records, so the loads return zeros
+    // without touching memory (re-reading a step with non-temporal loads would go to HBM)
+    auto issue_at = [&](int t0_in, long long phys, U32x4 (&kb)[UMAX][NC], U32x4 (&vb)[UMAX][NC], bool live) {
         const int t0 = __builtin_amdgcn_readfirstlane(t0_in);
         const char* kbase = p.pool + (phys * p.page_elems + head_off +
                                       static_cast<long long>(t0 & (kPageTokens - 1)) * D) * ESZ;
@@ -343,7 +346,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
         // covers whole 128-byte lines, so nothing is lost by not keeping them (C2 fp32 B1:
         // 47.1-47.5 vs 51.4-52.2 us per call).
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<char*>(kbase), 0, 0x7FFFFFFF, kBufferFlags);
+            const_cast<char*>(kbase), 0, live ? 0x7FFFFFFF : 0, kBufferFlags);
         const uint32_t vplane = static_cast<uint32_t>(p.plane_elems * ESZ);
 #pragma unroll
         for (int u = 0; u < UMAX; ++u) {
@@ -442,20 +445,19 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
                 }
     };
 
-    // ---- software-pipelined stream.  Every step issues the same number of loads
-    // (past the end it re-reads the step just computed, which L2 still holds), so
-    // the compiler's load counting stays exact and each step waits only for its own
-    // loads.
-    issue_at(step_t0(0), phys_of(step_t0(0)), kbuf[0], vbuf[0]);
+    // ---- software-pipelined stream.  Every step issues the same number of loads (past
+    // the end with an empty buffer range: no memory access), so the compiler's load
+    // counting stays exact and each step waits only for its own loads.
+    issue_at(step_t0(0), phys_of(step_t0(0)), kbuf[0], vbuf[0], true);
     load_q();
 #pragma unroll
     for (int i = 1; i < kPrefetch; ++i) {
         const int t0 = step_t0(min(i, nsteps - 1));
-        issue_at(t0, phys_of(t0), kbuf[i], vbuf[i]);
+        issue_at(t0, phys_of(t0), kbuf[i], vbuf[i], i < nsteps);
     }
     // Unrolled by the buffer count so every buffer index is a constant: step s0 + k is
     // computed from buffer k while step nxt(s0 + k) = s0 + k + kPrefetch is loaded into the
-    // buffer computed last (past the end, the step being computed is loaded again).  The
+    // buffer computed last (past the end, an empty load of the step being computed).  The
     // page-table entry of each issued step is loaded one issue ahead, so its latency never
     // holds the loads back.  Exits only through the goto: the back-edge is steady state.
     auto nxt = [&](int i) { return i + kPrefetch < nsteps ? i + kPrefetch : i; };
@@ -466,7 +468,7 @@ __global__ void __launch_bounds__(kThreads) decode_stream_kernel(const DecodeK p
             const long long ph = ph_next;
             ph_next = phys_of(step_t0(nxt(s0 + k + 1)));
             issue_at(step_t0(nxt(s0 + k)), ph, kbuf[(k + kPrefetch) % kStreamBuffers],
-                     vbuf[(k + kPrefetch) % kStreamBuffers]);
+                     vbuf[(k + kPrefetch) % kStreamBuffers], s0 + k + kPrefetch < nsteps);
             // the loads leave before any use of the step being computed, so that waiting
             // for that step never holds back the next one
             __builtin_amdgcn_sched_barrier(0);
@@ -637,13 +639,15 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     // previous step's loads were still writing made the compiler drain every load in
     // flight at the loop head).  A step is 32 x D contiguous elements of each plane.
     const uint32_t lane16 = static_cast<uint32_t>(16 * lane);
-    auto issue_at = [&](int st, long long phys, int buf) {
+    // live = false: a step past the end (see decode_stream_kernel): no records, no access
+    auto issue_at = [&](int st, long long phys, int buf, bool live) {
         const int t0 = __builtin_amdgcn_readfirstlane(step_t0(st));  // a step never crosses a page
         const int slot0 = t0 & (kPageTokens - 1);
         const char* kp = p.pool + (phys * p.page_elems + kblk + static_cast<long long>(slot0) * D) * 2;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kp), 0, 0x7FFFFFFF, kBufferFlags);
+        const int range = live ? 0x7FFFFFFF : 0;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kp), 0, range, kBufferFlags);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<char*>(kp + p.plane_elems * 2), 0, 0x7FFFFFFF, kBufferFlags);
+            const_cast<char*>(kp + p.plane_elems * 2), 0, range, kBufferFlags);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -654,7 +658,7 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         for (int dt = 0; dt < NDT; ++dt)
             vb[buf][dt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane16, 1024 * dt, kCacheNt));
     };
-    if (nst > 0) issue_at(wave, phys_of(wave), 0);
+    if (nst > 0) issue_at(wave, phys_of(wave), 0, true);
 
     // ---- q of head h0 + n (zero for padding columns), log2 units, split into hi + lo
     const float* qb = p.q + static_cast<size_t>(b) * p.heads * D;
@@ -754,8 +758,8 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
     };
 
     // ---- pipeline over this wave's steps with two register buffers (one step in flight
-    // ahead of the one computed); every iteration issues the same loads (past the end it
-    // re-reads a step already loaded) so the compiler's load counting stays exact.  The
+    // ahead of the one computed); every iteration issues the same loads (past the end
+    // empty ones) so the compiler's load counting stays exact.  The
     // loads of the next step leave before any MFMA of the current one (scheduling barrier)
     // and the page-table entry of each issued step is loaded one issue ahead.
     auto gstep = [&](int i) { return wave + kWaves * min(i, nst - 1); };
@@ -764,13 +768,13 @@ __global__ void __launch_bounds__(kThreads, kMfmaWgPerCu) decode_mfma_kernel(con
         for (int i = 0;; i += 2) {
             long long ph = ph_next;
             ph_next = phys_of(gstep(i + 2));
-            issue_at(gstep(i + 1), ph, 1);
+            issue_at(gstep(i + 1), ph, 1, i + 1 < nst);
             __builtin_amdgcn_sched_barrier(0);
             compute(gstep(i), 0);
             if (i + 1 >= nst) break;
             ph = ph_next;
             ph_next = phys_of(gstep(i + 3));
-            issue_at(gstep(i + 2), ph, 0);
+            issue_at(gstep(i + 2), ph, 0, i + 2 < nst);
             __builtin_amdgcn_sched_barrier(0);
             compute(gstep(i + 1), 1);
             if (i + 2 >= nst) break;
