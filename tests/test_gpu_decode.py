@@ -111,7 +111,7 @@ def test_decode_shapes(gpu, heads, kv_heads, D, seq):
     (1, 1, 64, 1),       # single position
 ])
 def test_decode_16bit_mfma_shapes(gpu, dtype, heads, kv_heads, D, seq):
-    """16-bit caches with head_dim 64/128 decode on MFMA tiles (V stored dims-major)
+    """16-bit caches with head_dim 64/128 decode on MFMA tiles (pages in the MFMA operand layout)
     with hi/lo-split q and P: still the fp32-accumulation tolerance."""
     q = normal(seq + 7, heads * D)
     Kb, K = to_dtype_bits(normal(seq + 8, (seq, kv_heads * D)), dtype)
