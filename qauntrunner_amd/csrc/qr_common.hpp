@@ -161,6 +161,11 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer resources and the cache-policy bits of the buffer intrinsics (gfx9 family).
+constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3
+constexpr int kCacheSc1 = 16;             // sc1: device scope
+constexpr int kCacheNt = 2;               // nt: streamed data, read once (whole lines per wave load)
+
 // ---------------------------------------------------------------- 16-byte vector loads
 struct alignas(16) U32x4 { uint32_t x, y, z, w; };
 

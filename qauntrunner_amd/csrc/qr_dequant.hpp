@@ -65,13 +65,13 @@ struct PtrRow {
 struct BufRow {
     __amdgpu_buffer_rsrc_t r;
     uint32_t so;  // byte offset of the row inside the buffer (uniform)
-    __device__ __forceinline__ uint32_t u8(int o) const { return __builtin_amdgcn_raw_buffer_load_b8(r, o, so, 0); }
-    __device__ __forceinline__ uint32_t u16(int o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, so, 0); }
-    __device__ __forceinline__ uint32_t u32(int o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, so, 0); }
-    __device__ __forceinline__ u32x4_t u128(int o) const { return __builtin_amdgcn_raw_buffer_load_b128(r, o, so, 0); }
+    __device__ __forceinline__ uint32_t u8(int o) const { return __builtin_amdgcn_raw_buffer_load_b8(r, o, so, kCacheNt); }
+    __device__ __forceinline__ uint32_t u16(int o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, so, kCacheNt); }
+    __device__ __forceinline__ uint32_t u32(int o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, so, kCacheNt); }
+    __device__ __forceinline__ u32x4_t u128(int o) const { return __builtin_amdgcn_raw_buffer_load_b128(r, o, so, kCacheNt); }
     __device__ __forceinline__ float2 f2(int o) const {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, o, so, 0);
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, o, so, kCacheNt);
         return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
     }
 };

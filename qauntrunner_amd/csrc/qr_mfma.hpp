@@ -49,9 +49,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 // this wave's LDS-DMA writes have all landed
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
-constexpr int kBufferFlags = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
-constexpr int kCacheSc1 = 16;             // buffer intrinsic cache-policy bits: sc1 (device scope)
-constexpr int kCacheNt = 2;               // buffer intrinsic cache-policy bits: nt (streamed, read once)
 
 // 16 bytes per lane from a raw buffer into LDS at lds + 16 * lane (buffer_load_dwordx4
 // ... lds); out-of-range offsets read zeros.  `lds` must be the same for every lane of

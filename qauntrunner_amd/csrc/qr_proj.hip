@@ -314,7 +314,7 @@ __device__ __forceinline__ void wuv_body(const MlaProjArgs& a, const WuvLayout& 
         const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t*>(g.src), static_cast<short>(0), nrows * static_cast<int>(a.row_bytes), kBufferFlags);
         for (int r = wave; r < kWuvRows; r += kWuvThreads / 64)
-            buffer_load_lds16(rw, reinterpret_cast<const char*>(lds) + r * L.lds_stride, voff,
+            buffer_load_lds16<kCacheNt>(rw, reinterpret_cast<const char*>(lds) + r * L.lds_stride, voff,
                               static_cast<uint32_t>(r * a.row_bytes));
         const char* ul = reinterpret_cast<const char*>(lds) + kWuvRows * L.lds_stride;
         const int pieces = g.cols * 4 / 1024;
