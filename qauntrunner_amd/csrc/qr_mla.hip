@@ -159,11 +159,15 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // and PV, so on every SIMD one wave's MFMAs run beside the other's softmax and loads.
 // A tile (32 latent rows, contiguous inside one page) is loaded into registers of
 // the PV waves two tiles ahead of its use and written to one of three LDS buffers.
-//   QK  wave w < 4 scores positions 16(w/2)..16(w/2)+15 of the tile for heads
-//       16(w%2)..16(w%2)+15: S^T[pos][head] = C[pos][dims] . q~^T[dims][head]; A is
-//       read from the row-major tile, B = the wave's 16 heads of q~ (hi + lo) stays in
-//       registers.  Raw scores go to LDS.
-//   Softmax (log2 units, online): PV wave v owns heads 8v..8v+7; it keeps their (m, l)
+//   QK  wave w < 4 scores positions 16(w%2)..16(w%2)+15 of the tile for all 32 heads
+//       over half of the latent's dims (k-steps of half w/2): S^T[pos][head] =
+//       C[pos][dims] . q~^T[dims][head]; A is read from the row-major tile once per
+//       k-step and feeds four MFMAs (two head tiles, hi + lo), B = the wave's half of q~
+//       (hi + lo) stays in registers.  Raw partial scores of each half go to LDS.
+//       (Waves owning 16 heads over all dims read every A operand twice per tile: C5
+//       24.0 vs 23.8 us per call.)
+//   Softmax (log2 units, online): PV wave v owns heads 8v..8v+7; it adds the two halves'
+//   scores, keeps their (m, l)
 //   and writes P (hi + lo parts) and the accumulator rescale factor of each head to
 //   LDS.
 //   PV  wave 4 + v owns latent dims 128v..128v+127 for all 32 heads:
@@ -271,8 +275,8 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     __shared__ __attribute__((aligned(1024))) char lds_b0[TB];
     __shared__ __attribute__((aligned(1024))) char lds_b1[TB];
     __shared__ __attribute__((aligned(1024))) char lds_b2[TB];
-    __shared__ __attribute__((aligned(16))) float lds_s0[kMHeads * kScoreStride];
-    __shared__ __attribute__((aligned(16))) float lds_s1[kMHeads * kScoreStride];
+    __shared__ __attribute__((aligned(16))) float lds_s0[2 * kMHeads * kScoreStride];  // k halves 0, 1
+    __shared__ __attribute__((aligned(16))) float lds_s1[2 * kMHeads * kScoreStride];
     __shared__ __attribute__((aligned(16))) char lds_p[2 * kMHeads * PR];  // P hi rows, then lo rows
     __shared__ float lds_corr[kMHeads];  // accumulator rescale factor of the tile
     __shared__ float lds_l[kMHeads];
@@ -338,8 +342,9 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     };
     TileRegs tr0, tr1;  // tiles in flight (PV waves)
 
-    // ---- B operands of QK: lane (q4, l16) of QK wave (ph, ht) = (w / 2, w % 2) holds
-    // dims 32kk + 8q4 .. +8 of head 16ht + l16, split into hi + lo parts of the cache type
+    // ---- B operands of QK: lane (q4, l16) of QK wave (kh, ph) = (w / 2, w % 2) holds, for
+    // k-step kk of its half and head tile ht, dims 32kk + 8q4 .. +8 of head 16ht + l16,
+    // split into hi + lo parts of the cache type
     // (fp16: after the per-head power-of-two scaling).  While the PV waves wait for the
     // first two tiles, the QK waves read q~ of the workgroup's 32 heads once, coalesced,
     // convert it to hi + lo and stage it in tile buffers 1 (hi) and 2 (lo), free until
@@ -399,20 +404,23 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
 
     // ================================================================ QK waves
     if (qk_wave) {
-        const int ht = wave & 1;   // head tile
-        const int ph = wave >> 1;  // position half of the tile
-        V qhi[NK], qlo[NK];
-        {
+        constexpr int NKH = NK / 2;   // k-steps of a half
+        static_assert(NK % 2 == 0, "k halves");
+        const int kh = wave >> 1;     // k half: k-steps NKH kh .. NKH kh + NKH - 1
+        const int ph = wave & 1;      // position half of the tile
+        V qhi[2][NKH], qlo[2][NKH];   // both head tiles
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht) {
             const int hr = 16 * ht + l16;
 #pragma unroll
-            for (int kk = 0; kk < NK; ++kk) {
-                const int c = (4 * kk + q4) ^ (hr & 7);
-                qhi[kk] = *reinterpret_cast<const V*>(lds_b1 + hr * QS + 16 * c);
-                qlo[kk] = *reinterpret_cast<const V*>(lds_b2 + hr * QS + 16 * c);
+            for (int kk = 0; kk < NKH; ++kk) {
+                const int c = (4 * (NKH * kh + kk) + q4) ^ (hr & 7);
+                qhi[ht][kk] = *reinterpret_cast<const V*>(lds_b1 + hr * QS + 16 * c);
+                qlo[ht][kk] = *reinterpret_cast<const V*>(lds_b2 + hr * QS + 16 * c);
             }
         }
-        // A operand: row 16ph + l16, logical chunk 4kk + q4 = block kk/2, slot
-        // 4 (kk & 1) + q4, stored at slot (4 (kk & 1) + q4) ^ f = 4 ((kk & 1) ^ (f >> 2)) +
+        // A operand of k-step kg: row 16ph + l16, logical chunk 4kg + q4 = block kg/2, slot
+        // 4 (kg & 1) + q4, stored at slot (4 (kg & 1) + q4) ^ f = 4 ((kg & 1) ^ (f >> 2)) +
         // (q4 ^ (f & 3)); f depends on l16 only (16ph is a multiple of 16).
         const int rq = 16 * ph + l16;
         const int fq = row_swizzle(rq);
@@ -420,25 +428,30 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
         const int qk_flip = fq >> 2;
         // raw scores of the tile in `tile` into `sbuf` (the softmax scales and masks)
         auto qk = [&](const char* tile, float* sbuf) __attribute__((always_inline)) {
-            f32x4_t sc[2], sl[2];  // hi / lo chains x parity of the k-step
+            f32x4_t sc[2], sl[2];  // hi / lo chains x head tile
 #pragma unroll
             for (int e = 0; e < 2; ++e) sc[e] = sl[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            U32x4 ra[NK];
+            U32x4 ra[NKH];
             auto load = [&](int kk) __attribute__((always_inline)) {
-                ra[kk] = *reinterpret_cast<const U32x4*>(tile + BB * (kk >> 1) + qk_off + 64 * ((kk & 1) ^ qk_flip));
+                const int kg = NKH * kh + kk;
+                ra[kk] = *reinterpret_cast<const U32x4*>(tile + BB * (kg >> 1) + qk_off + 64 * ((kg & 1) ^ qk_flip));
             };
 #pragma unroll
             for (int kk = 0; kk < kQkAhead; ++kk) load(kk);
 #pragma unroll
-            for (int kk = 0; kk < NK; ++kk) {
-                if (kk + kQkAhead < NK) load(kk + kQkAhead);
+            for (int kk = 0; kk < NKH; ++kk) {
+                if (kk + kQkAhead < NKH) load(kk + kQkAhead);
                 const V av = __builtin_bit_cast(V, ra[kk]);
-                sc[kk & 1] = MT::mma(av, qhi[kk], sc[kk & 1]);
-                sl[kk & 1] = MT::mma(av, qlo[kk], sl[kk & 1]);
+                sc[0] = MT::mma(av, qhi[0][kk], sc[0]);
+                sc[1] = MT::mma(av, qhi[1][kk], sc[1]);
+                sl[0] = MT::mma(av, qlo[0][kk], sl[0]);
+                sl[1] = MT::mma(av, qlo[1][kk], sl[1]);
             }
-            // lane holds positions 16ph + 4q4 + r of head 16ht + l16
-            *reinterpret_cast<f32x4_t*>(sbuf + (16 * ht + l16) * kScoreStride + 16 * ph + 4 * q4) =
-                (sc[0] + sc[1]) + (sl[0] + sl[1]);
+            // lane holds positions 16ph + 4q4 + r of heads 16ht + l16, k half kh
+            float* sb = sbuf + kh * kMHeads * kScoreStride;
+#pragma unroll
+            for (int ht = 0; ht < 2; ++ht)
+                *reinterpret_cast<f32x4_t*>(sb + (16 * ht + l16) * kScoreStride + 16 * ph + 4 * q4) = sc[ht] + sl[ht];
         };
         qk(lds_b0, lds_s0);
         lds_barrier();  // q~ read by every QK wave: buffer 1 may be refilled
@@ -507,8 +520,9 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
 
         // ---- softmax of tile t for head hs (only the last tile can be partial)
         {
-            const float4 r = *reinterpret_cast<const float4*>(s_cur + hs * kScoreStride + 4 * i8);
-            float v[4] = {r.x * sscale, r.y * sscale, r.z * sscale, r.w * sscale};
+            const float4 r0 = *reinterpret_cast<const float4*>(s_cur + hs * kScoreStride + 4 * i8);
+            const float4 r1 = *reinterpret_cast<const float4*>(s_cur + (kMHeads + hs) * kScoreStride + 4 * i8);
+            float v[4] = {(r0.x + r1.x) * sscale, (r0.y + r1.y) * sscale, (r0.z + r1.z) * sscale, (r0.w + r1.w) * sscale};
             if (t0 + kMTile > t_end) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
