@@ -193,10 +193,11 @@ __global__ void __launch_bounds__(kThreads) mla_combine_kernel(const MlaK p) {
 // (fp16) significant bits; for fp16 caches q~ is first multiplied per head by the
 // power of two that brings its largest element to at most 2^14 (exact, scores scaled
 // back), so it cannot overflow.  PV: P (at most 2^8 with the lazy rescale below) also
-// enters as hi + lo parts of the cache type.  Split partials are stored normalised (u_s = acc / l) in
-// fp16 times a per-(head, split) power of two chosen from the largest |u_s| of the
-// head, so they neither overflow nor lose their small values whatever the latent's
-// range (a bf16 latent may hold values far outside fp16's range).
+// enters as hi + lo parts of the cache type.  Split partials (the unnormalised
+// accumulators) are stored in fp16 times a power of two per (head, split, 128-dim
+// block) chosen from the block's largest value, so they neither overflow nor lose their
+// small values whatever the latent's range (a bf16 latent may hold values far outside
+// fp16's range).
 // LDS tile layout: blocks of 8 logical 16-byte chunks (128 bytes) x 32 rows; inside
 // a block, chunk c of row r sits at slot (c % 8) ^ f(r), where f(r) is the 3-bit
 // reversal of (r >> 1) & 7, so the 16 rows of a QK read and the 8 rows of half a
@@ -243,8 +244,9 @@ struct MlaMK {
     const float* q_tilde;
     const float* q_rope;
     float* u;
-    void* part_u;      // [heads][splits][kv_lora] fp16: u_s / 2^e
-    float4* part_ml;   // [heads][splits] (m, l, e, 0)
+    void* part_u;      // [heads][splits][kv_lora] fp16: acc_s / 2^e (unnormalised)
+    float2* part_ml;   // [heads][splits] (m, l)
+    signed char* part_e;  // [heads][splits][4] e of each 128-dim block
     float qscale;      // scale * log2(e)
 };
 
@@ -280,7 +282,6 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
     __shared__ __attribute__((aligned(16))) char lds_p[2 * kMHeads * PR];  // P hi rows, then lo rows
     __shared__ float lds_corr[kMHeads];  // accumulator rescale factor of the tile
     __shared__ float lds_l[kMHeads];
-    __shared__ float lds_amax[4][kMHeads];
     __shared__ int lds_qexp[kMHeads];
 
     // Launch slot b runs on XCD b % 8; consecutive logical indices (the head groups
@@ -471,9 +472,7 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
             QR_QK_STEP(t + 5, lds_b0, lds_s0)
 #undef QR_QK_STEP
         }
-        lds_barrier();  // l published
-        lds_barrier();  // amax published
-        lds_barrier();  // partial rows staged
+        if (nsplit == 1) lds_barrier();  // l published
         return;
     }
 
@@ -599,100 +598,91 @@ __global__ void __launch_bounds__(kMWaves * 64) mla_tile_kernel(const MlaMK p) {
         if (t + 6 >= ntiles) break;
     }
 
-    // l of heads 16nt + l16, from the lanes that own them
-    if (i8 == 0) lds_l[hs] = l_s;
-    lds_barrier();  // l published
-    float l[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) l[nt] = lds_l[16 * nt + l16];
     if (nsplit == 1) {
+        // l of heads 16nt + l16, from the lanes that own them
+        if (i8 == 0) lds_l[hs] = l_s;
+        lds_barrier();  // l published
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int head = hg * kMHeads + 16 * nt + l16;
             if (head >= p.heads) continue;
             float* out = p.u + static_cast<size_t>(head) * KL + 128 * pw + 4 * q4;
-            const float inv = 1.f / l[nt];
+            const float inv = 1.f / lds_l[16 * nt + l16];
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt)
                 *reinterpret_cast<float4*>(out + 16 * dt) =
                     make_float4(acc[nt][dt][0] * inv, acc[nt][dt][1] * inv, acc[nt][dt][2] * inv, acc[nt][dt][3] * inv);
         }
-        lds_barrier();  // matches the QK waves' barriers
-        lds_barrier();
         return;
     }
-    // Normalised split result u_s = acc / l, stored as fp16 u_s / 2^e with e per (head,
-    // split) such that the head's largest |u_s| lands in [2^14, 2^15): no overflow and
-    // full fp16 precision whatever the latent's range.  A lane holds 4 dims of each of 8
-    // dim tiles of its head, so it would store 8 bytes into each of 16 head rows per
-    // instruction; the rows are assembled in LDS first (heads 0-15 in tile buffer 0,
-    // 16-31 in buffer 1, both free after the last step) and every wave store then
-    // writes one whole 1 KiB head row.
-    constexpr int SR = KL * 2 + 16;  // staged row pitch (bytes)
-    static_assert(16 * SR <= TB, "16 staged partial rows must fit in one tile buffer");
-    float inv[2];
+    // Split partial: the unnormalised accumulators, stored as fp16 acc / 2^e with e per
+    // (head, split, this wave's 128 dims) such that the block's largest |acc| lands in
+    // [2^14, 2^15): no overflow and full fp16 precision whatever the latent's range.  The
+    // wave assembles its 32 head segments (256 bytes each) in its own part of a tile
+    // buffer no step uses any more (the buffer after the last tile's), so the epilogue
+    // needs no workgroup barrier: every wave store then writes four whole segments.
+    // Two tile buffers are free once the last step begins (the buffers of the two tiles
+    // after the last): waves 0-1 stage in one, waves 2-3 in the other.
+    // (m, l) of each head come from the softmax lanes that own them.
+    {
+        const int head = hg * kMHeads + hs;
+        if (i8 == 0 && head < p.heads)
+            p.part_ml[static_cast<size_t>(head) * p.splits + split] = make_float2(m_s, l_s);
+    }
+    constexpr int SRW = 256 + 16;  // staged segment pitch (bytes)
+    static_assert(2 * kMHeads * SRW <= TB, "two waves' staged segments fit in one tile buffer");
+    const int fb = (ntiles + (pw >> 1)) % 3;  // tile t's buffer is t % 3
+    char* stage = (fb == 0 ? lds_b0 : fb == 1 ? lds_b1 : lds_b2) + (pw & 1) * kMHeads * SRW;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        inv[nt] = 1.f / l[nt];
         float amax = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(acc[nt][dt][r] * inv[nt]));
+            for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(acc[nt][dt][r]));
         amax = max_xor32(max_xor16(amax));
-        if (q4 == 0) lds_amax[pw][16 * nt + l16] = amax;
-    }
-    lds_barrier();  // amax published
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+        // e = floor(log2(amax)) - 14 for finite non-zero amax (subnormals included),
+        // at least -128 (values below 2^-114 then still land above fp16's subnormals)
+        const int e = amax > 0.f && amax <= 3.4e38f ? max(ilogbf(amax) - 14, -128) : 0;
         const int hl = 16 * nt + l16;
-        const float amax = fmaxf(fmaxf(lds_amax[0][hl], lds_amax[1][hl]), fmaxf(lds_amax[2][hl], lds_amax[3][hl]));
-        // e = floor(log2(amax)) - 14 for finite non-zero amax (subnormals included)
-        const int e = amax > 0.f && amax <= 3.4e38f ? ilogbf(amax) - 14 : 0;
-        char* stage = (nt ? lds_b1 : lds_b0) + l16 * SR;
+        const int head = hg * kMHeads + hl;
+        if (q4 == 0 && head < p.heads)
+            p.part_e[(static_cast<size_t>(head) * p.splits + split) * 4 + pw] = static_cast<signed char>(e);
+        char* row = stage + hl * SRW;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             typedef float f32x2_t __attribute__((ext_vector_type(2)));
             typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-            const f16x2_t lo = __builtin_convertvector(
-                f32x2_t{ldexpf(acc[nt][dt][0] * inv[nt], -e), ldexpf(acc[nt][dt][1] * inv[nt], -e)}, f16x2_t);
-            const f16x2_t hi = __builtin_convertvector(
-                f32x2_t{ldexpf(acc[nt][dt][2] * inv[nt], -e), ldexpf(acc[nt][dt][3] * inv[nt], -e)}, f16x2_t);
-            *reinterpret_cast<uint2*>(stage + 2 * (128 * pw + 16 * dt + 4 * q4)) =
+            const f16x2_t lo = __builtin_convertvector(f32x2_t{ldexpf(acc[nt][dt][0], -e), ldexpf(acc[nt][dt][1], -e)}, f16x2_t);
+            const f16x2_t hi = __builtin_convertvector(f32x2_t{ldexpf(acc[nt][dt][2], -e), ldexpf(acc[nt][dt][3], -e)}, f16x2_t);
+            *reinterpret_cast<uint2*>(row + 2 * (16 * dt + 4 * q4)) =
                 make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
         }
     }
-    {
-        // (m, l, e) of head hs, from the lanes that own it
-        const float amax = fmaxf(fmaxf(lds_amax[0][hs], lds_amax[1][hs]), fmaxf(lds_amax[2][hs], lds_amax[3][hs]));
-        const int e = amax > 0.f && amax <= 3.4e38f ? ilogbf(amax) - 14 : 0;
-        const int head = hg * kMHeads + hs;
-        if (i8 == 0 && head < p.heads)
-            p.part_ml[static_cast<size_t>(head) * p.splits + split] = make_float4(m_s, l_s, static_cast<float>(e), 0.f);
-    }
-    lds_barrier();  // partial rows staged
-    // PV wave pw writes head rows pw, pw + 4, ...: lane j the 16 bytes at 16 j
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // store i: segments of heads 4i .. 4i + 3, lane j the 16 bytes at 16 (j % 16) of head
+    // 4i + j / 16, written through to device scope (sc1)
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int i = 0; i < kMHeads / 4; ++i) {
-        const int hl = pw + 4 * i;
+        const int hl = 4 * i + (lane >> 4);
         const int head = hg * kMHeads + hl;
-        if (head >= p.heads) break;
-        const char* stage = (hl < 16 ? lds_b0 : lds_b1) + (hl & 15) * SR;
-        const U32x4 v = *reinterpret_cast<const U32x4*>(stage + 16 * lane);
-        // written through the XCD's L2 (sc1), so the kernel's end has no dirty partial
-        // lines to write back before the merge starts (C5: ~0.5 us per call against
-        // write-back stores; non-temporal stores were slower)
-        char* prow = static_cast<char*>(p.part_u) + (static_cast<size_t>(head) * p.splits + split) * (KL * 2);
-        typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-        const __amdgpu_buffer_rsrc_t rrow = __builtin_amdgcn_make_buffer_rsrc(prow, 0, KL * 2, kBufferFlags);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, v), rrow, 16 * lane, 0, kCacheSc1);
+        const U32x4 v = *reinterpret_cast<const U32x4*>(stage + hl * SRW + 16 * (lane & 15));
+        if (head < p.heads) {
+            char* seg = static_cast<char*>(p.part_u) + ((static_cast<size_t>(head) * p.splits + split) * KL + 128 * pw) * 2;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(seg, 0, 256, kBufferFlags);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, v), rs, 16 * (lane & 15), 0, kCacheSc1);
+        }
     }
 }
 
 // Split merge for the MFMA path: one workgroup per (head, 64-dim block); thread (grp, c8)
 // owns 8 dims (one 16-byte load of fp16 partials per split) and splits grp, grp + 32, ...,
 // all loads of a batch issued at once (in range: a repeated split weighs zero); split s
-// weighs l_s 2^(m_s - M) and its stored values 2^e_s.  The 32 split groups are merged
+// weighs 2^(m_s - M), its stored values 2^(e of their 128-dim block), its sum l_s
+// 2^(m_s - M) goes to the denominator.  The 32 split groups are merged
 // through LDS.  (Against one workgroup per 128-dim block with 8-byte loads: C5 24.4 vs
 // 25.1 us per call.)
 __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
@@ -711,19 +701,22 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
     float m = -INFINITY, l = 0.f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     constexpr int kB = 4;
+    const int eb = blk >> 1;  // 128-dim block of the exponent
     for (int s0 = grp; s0 < nsplit; s0 += 32 * kB) {
         uint4 a[kB];
-        float4 ml[kB];
+        float2 ml[kB];
+        int ex[kB];
 #pragma unroll
         for (int i = 0; i < kB; ++i) {
             const int s = min(s0 + 32 * i, nsplit - 1);
             a[i] = *reinterpret_cast<const uint4*>(part + (base + s) * KL + d);
             ml[i] = p.part_ml[base + s];
+            ex[i] = p.part_e[(base + s) * 4 + eb];
         }
         float mb = m;
 #pragma unroll
         for (int i = 0; i < kB; ++i) {
-            if (s0 + 32 * i >= nsplit) ml[i] = make_float4(-INFINITY, 0.f, 0.f, 0.f);
+            if (s0 + 32 * i >= nsplit) ml[i] = make_float2(-INFINITY, 0.f);
             mb = fmaxf(mb, ml[i].x);
         }
         const float cm = m == -INFINITY ? 0.f : fast_exp2(m - mb);
@@ -732,11 +725,11 @@ __global__ void __launch_bounds__(256) mla_combine_wide_kernel(const MlaMK p) {
         for (int k = 0; k < 8; ++k) o[k] *= cm;
 #pragma unroll
         for (int i = 0; i < kB; ++i) {
-            const float w = ml[i].x == -INFINITY ? 0.f : ml[i].y * fast_exp2(ml[i].x - mb);
-            const float wv = ldexpf(w, static_cast<int>(ml[i].z));  // weight of the stored values
+            const float w = ml[i].x == -INFINITY ? 0.f : fast_exp2(ml[i].x - mb);
+            const float wv = ldexpf(w, ex[i]);  // weight of the stored values
             typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
             const h8_t v = __builtin_bit_cast(h8_t, a[i]);
-            l += w;
+            l = fmaf(ml[i].y, w, l);
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[k] = fmaf(static_cast<float>(v[k]), wv, o[k]);
         }
@@ -803,8 +796,9 @@ MlaPlan plan_mla(const MlaArgs& a) {
     pl.splits = (a.seq_len + pl.split_tokens - 1) / pl.split_tokens;
     const size_t slots = static_cast<size_t>(a.heads) * pl.splits;
     const size_t part_elem = mfma_eligible(a) ? 2 : 4;   // fp16 partials on the MFMA path
-    const size_t ml_bytes = mfma_eligible(a) ? 16 : 8;  // (m, l, e, 0) / (m, l)
-    pl.workspace_bytes = (pl.splits > 1 ? align256(slots * a.kv_lora * part_elem) + align256(slots * ml_bytes) : 0) + q_copy;
+    const size_t ml_bytes = 8;                          // (m, l)
+    const size_t e_bytes = mfma_eligible(a) ? align256(slots * 4) : 0;  // exponents of the fp16 partials
+    pl.workspace_bytes = (pl.splits > 1 ? align256(slots * a.kv_lora * part_elem) + align256(slots * ml_bytes) + e_bytes : 0) + q_copy;
     return pl;
 }
 
@@ -832,9 +826,10 @@ hipError_t launch_mla(const MlaArgs& a, const MlaPlan& pl, void* workspace, hipS
         k.groups = (a.heads + kMHeads - 1) / kMHeads;
         k.per_xcd = (k.groups * pl.splits + 7) / 8;
         k.u = a.u;
-        const size_t part_bytes = pl.splits > 1 ? align256(slots * a.kv_lora * 2) + align256(slots * 16) : 0;
+        const size_t part_bytes = pl.splits > 1 ? align256(slots * a.kv_lora * 2) + align256(slots * 8) + align256(slots * 4) : 0;
         k.part_u = ws;
-        k.part_ml = reinterpret_cast<float4*>(ws + align256(slots * a.kv_lora * 2));
+        k.part_ml = reinterpret_cast<float2*>(ws + align256(slots * a.kv_lora * 2));
+        k.part_e = reinterpret_cast<signed char*>(ws + align256(slots * a.kv_lora * 2) + align256(slots * 8));
         // the kernel reads q~ / q_rope as float4
         k.q_tilde = a.q_tilde;
         k.q_rope = a.q_rope;
