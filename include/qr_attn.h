@@ -82,10 +82,10 @@ const char* qr_status_name(int status);
 /* ctor PagedKvCache(layers, heads, kvHeads, headDim, maxSeq), PagedKvCache.cs:29-37.
  * kv_dtype: QR_DTYPE_F32 (the reference's page type, PagedKvCache.cs:17-18),
  * F16 or BF16.  max_batch: number of independent sequences (seq_id 0..max_batch-1),
- * each with its own page table; 1 reproduces the reference.  head_dim: a multiple
- * of 8 from 16 to 256 (the reference takes any; model head sizes are multiples of 8).
- * 16-bit caches with head_dim 64 or 128 decode on MFMA tiles; every other shape on the
- * fp32 streaming kernel. */
+ * each with its own page table; 1 reproduces the reference.  head_dim: any size from
+ * 1 to 512 (the reference takes any).  16-bit caches with head_dim 64 or 128 decode on
+ * MFMA tiles; multiples of 8 from 16 to 256 on the streaming kernel; every other size on
+ * a scalar generic kernel (correct, not tuned: no model uses such sizes). */
 int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim, int max_seq,
                  int kv_dtype, int max_batch);
 int qr_kv_destroy(qr_kv* kv);

@@ -313,6 +313,70 @@ __global__ void __launch_bounds__(256) rope_append_kernel(const RopeAppendArgs a
     }
 }
 
+// A float into the cache dtype (the append codecs).
+__device__ __forceinline__ void store1(void* pool, int dtype, long long j, float x) {
+    switch (dtype) {
+        case QR_DTYPE_F32: static_cast<float*>(pool)[j] = x; break;
+        case QR_DTYPE_F16: static_cast<uint16_t*>(pool)[j] = f32_to_f16_bits_ref(x); break;
+        default: static_cast<uint16_t*>(pool)[j] = f32_to_bf16_bits_ref(x); break;
+    }
+}
+
+// Any head size the item kernels do not take (not a multiple of 8, or above 256): one
+// workgroup per position, one thread per rotation pair (i, i + D/2) of a head, with the same
+// separately rounded products and sums; an odd head size leaves dim D - 1 unrotated, as the
+// reference rotates i < D/2 only (TransformerOps.cs:78-87).  V rows (and dim D - 1 of
+// each K row) are copied in a second loop.
+__global__ void __launch_bounds__(256) rope_append_generic_kernel(const RopeAppendArgs a) {
+    const AppendArgs& g = a.app;
+    int pos0 = g.pos0;
+    if (g.pos_dev) {  // device-side position: written only where the pages of all rows were claimed
+        pos0 = *g.pos_dev;
+        if (pos0 < 0 || pos0 > g.max_seq - g.n || ((pos0 + g.n - 1) >> kPageShift) >= *g.held_dev) return;
+    }
+    const int D = g.geom.head_dim;
+    const int half = D >> 1;
+    const int kv_heads = g.geom.kv_heads;
+    const int q_heads = a.q ? a.q_width / D : 0;
+    const long long row = blockIdx.x;
+    const int t = pos0 + static_cast<int>(row);
+    __shared__ float cs[2][kMaxRopeHalf];
+    for (int i = threadIdx.x; i < half; i += 256) {
+        const float ang = mul_rn(static_cast<float>(t), a.freq[i]);
+        cs[0][i] = cosf(ang);
+        cs[1][i] = sinf(ang);
+    }
+    __syncthreads();
+    const long long phys = g.page_table[t >> kPageShift];
+    const int slot = t & (kPageTokens - 1);
+    const float* krow = static_cast<const float*>(g.src[0]) + row * g.src_stride;
+    const float* vrow = static_cast<const float*>(g.src[1]) + row * g.src_stride;
+    const int pairs = (kv_heads + q_heads) * half;
+    for (int it = threadIdx.x; it < pairs; it += 256) {
+        const int h = it / half;
+        const int i = it - h * half;
+        float* q = h < kv_heads ? nullptr : a.q + row * a.q_width + (h - kv_heads) * D;
+        const float* src = q ? q : krow + h * D;
+        const float x0 = src[i], x1 = src[i + half];
+        const float c = cs[0][i], sn = cs[1][i];
+        const float y0 = sub_rn(mul_rn(x0, c), mul_rn(x1, sn));
+        const float y1 = add_rn(mul_rn(x0, sn), mul_rn(x1, c));
+        if (q) {
+            q[i] = y0;
+            q[i + half] = y1;
+        } else {
+            store1(g.pool, g.dtype, g.geom.offset(phys, 0, h, slot, i), y0);
+            store1(g.pool, g.dtype, g.geom.offset(phys, 0, h, slot, i + half), y1);
+        }
+    }
+    for (int it = threadIdx.x; it < kv_heads * D; it += 256) {
+        const int h = it / D;
+        const int d = it - h * D;
+        store1(g.pool, g.dtype, g.geom.offset(phys, 1, h, slot, d), vrow[h * D + d]);
+        if (d == 2 * half) store1(g.pool, g.dtype, g.geom.offset(phys, 0, h, slot, d), krow[h * D + d]);  // odd D
+    }
+}
+
 __global__ void __launch_bounds__(256) widen_kernel(const void* src, int dtype, float* dst, long long n) {
     for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += static_cast<long long>(gridDim.x) * 256)
         dst[i] = load_f32(src, dtype, i);
@@ -373,6 +437,11 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream) {
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream) {
     if (a.app.n == 0) return hipSuccess;
     const int D = a.app.geom.head_dim;
+    if (rope_generic(D)) {
+        if (D > 2 * kMaxRopeHalf) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(rope_append_generic_kernel, dim3(a.app.n), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
     const int heads = a.app.geom.kv_heads + (a.q ? a.q_width / D : 0);
     const int ipt = rope_items_per_thread(heads, D);
     // V tiles: 16-bit MFMA-layout V plane (head_dim 64 or 128), kVTileTpt tokens per thread

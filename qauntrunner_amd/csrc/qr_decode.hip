@@ -909,6 +909,116 @@ __global__ void __launch_bounds__(kThreads) decode_combine_kernel(const DecodeK 
     }
 }
 
+// ---- any head size the vector kernels do not take (not a multiple of 8, or outside
+// 16..256): scalar split kernel.  One workgroup per (split, head, entry): the query row in
+// LDS, one position per thread for the scores (staged in LDS), the split's max and sum by
+// block reductions, then one dim per thread for the weighted sum of the V rows.  Partials
+// as the other decode kernels' ([nb][heads][split_stride][head_dim] unnormalised, (max,
+// sum) in log2 units), merged by decode_generic_combine_kernel.  Correct rather than
+// fast: no model uses such head sizes, the reference accepts them (PagedKvCache.cs:29-37,
+// SimdMath.cs:36-52 with its scalar tail).
+constexpr int kGenericMaxSplitTokens = 16 * kPageTokens;  // the plan's longest split
+
+__device__ __forceinline__ float load_cache(const char* pool, int dtype, long long i) {
+    switch (dtype) {
+        case QR_DTYPE_F32: return reinterpret_cast<const float*>(pool)[i];
+        case QR_DTYPE_F16: return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(pool)[i]);
+        default: return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(pool)[i]);
+    }
+}
+
+__device__ __forceinline__ float block_max(float x, float* red) {
+    x = fmaxf(x, dpp_xor1(x));
+    x = fmaxf(x, dpp_xor2(x));
+    x = fmaxf(x, dpp_half_mirror(x));
+    x = fmaxf(x, dpp_mirror(x));
+    x = max_xor32(max_xor16(x));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ float block_sum(float x, float* red) {
+    x = group_sum(x, 16);
+    x = sum_xor32(sum_xor16(x));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ void __launch_bounds__(kThreads) decode_generic_kernel(const DecodeK p, int dtype) {
+    static_assert(kThreads == 4 * 64, "block reductions over four waves");
+    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int seq = entry_seq(p, b);
+    const int st = entry_split_tokens(p, seq);
+    const int nsplit = (seq + st - 1) / st;
+    if (split >= nsplit) return;
+    const int t0 = split * st;
+    const int t1 = min(seq, t0 + st);
+    const int D = p.head_dim;
+    const int kvh = static_cast<int>(static_cast<long long>(h) * p.kv_heads / p.heads);
+    __shared__ float qs[kGenericMaxDim];
+    __shared__ float sc[kGenericMaxSplitTokens];
+    __shared__ float red[kWaves];
+    const size_t row = static_cast<size_t>(b) * p.heads + h;
+    for (int d = threadIdx.x; d < D; d += kThreads) qs[d] = p.q[row * D + d];
+    __syncthreads();
+    const int* pt = p.page_table + p.pt_off[b];
+    const long long head_off = static_cast<long long>(kvh) * kPageTokens * D;
+    float mx = -INFINITY;
+    for (int t = t0 + threadIdx.x; t < t1; t += kThreads) {
+        const long long k0 = pt[t >> kPageShift] * p.page_elems + head_off + static_cast<long long>(t & (kPageTokens - 1)) * D;
+        float s = 0.f;
+        for (int d = 0; d < D; ++d) s = fmaf(qs[d], load_cache(p.pool, dtype, k0 + d), s);
+        s *= p.qscale;
+        sc[t - t0] = s;
+        mx = fmaxf(mx, s);
+    }
+    const float M = block_max(mx, red);
+    float l = 0.f;
+    for (int t = t0 + threadIdx.x; t < t1; t += kThreads) {
+        const float e = fast_exp2(sc[t - t0] - M);
+        sc[t - t0] = e;
+        l += e;
+    }
+    const float L = block_sum(l, red);  // its barriers also publish the weights
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+        float acc = 0.f;
+        for (int t = t0; t < t1; ++t) {
+            const long long v0 = pt[t >> kPageShift] * p.page_elems + p.plane_elems + head_off +
+                                 static_cast<long long>(t & (kPageTokens - 1)) * D;
+            acc = fmaf(sc[t - t0], load_cache(p.pool, dtype, v0 + d), acc);
+        }
+        if (nsplit == 1) p.out[row * D + d] = acc / L;
+        else p.part_acc[(row * p.split_stride + split) * D + d] = acc;
+    }
+    if (nsplit > 1 && threadIdx.x == 0) p.part_ml[row * p.split_stride + split] = make_float2(M, L);
+}
+
+// Merge of the generic kernel's splits: one workgroup per (head, entry).
+__global__ void __launch_bounds__(kThreads) decode_generic_combine_kernel(const DecodeK p) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int seq = entry_seq(p, b);
+    const int st = entry_split_tokens(p, seq);
+    const int nsplit = (seq + st - 1) / st;
+    if (nsplit == 1) return;  // the split kernel wrote the output
+    const int D = p.head_dim;
+    const size_t row = static_cast<size_t>(b) * p.heads + h;
+    const size_t base = row * p.split_stride;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.part_ml[base + s].x);
+    float L = 0.f;
+    for (int s = 0; s < nsplit; ++s) L = fmaf(p.part_ml[base + s].y, fast_exp2(p.part_ml[base + s].x - M), L);
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+        float o = 0.f;
+        for (int s = 0; s < nsplit; ++s)
+            o = fmaf(p.part_acc[(base + s) * D + d], fast_exp2(p.part_ml[base + s].x - M), o);
+        p.out[row * D + d] = o / L;
+    }
+}
+
 int pick_gmax(int group) {
     if (group <= 1) return 1;
     if (group <= 2) return 2;
@@ -1078,7 +1188,8 @@ DecodePlan plan_decode(const DecodeArgs& a) {
     // kernel is faster.
     const int pairs = pl.units * a.nb;
     const int unit_heads = per_head ? 1 : std::min(gmax, group);
-    pl.fused = pl.max_splits > 1 && static_cast<long long>(pl.max_splits) * pairs <= cu_count() &&
+    pl.fused = !decode_generic(a.geom.head_dim) && pl.max_splits > 1 &&
+               static_cast<long long>(pl.max_splits) * pairs <= cu_count() &&
                unit_heads * a.geom.head_dim <= 1024 && pairs <= kDecodeCounters;
     // XCD-local slots need whole XCD rounds of pairs with equal head counts
     pl.xmap = pl.fused && pairs % 8 == 0 && (per_head || group % gmax == 0 || group < gmax);
@@ -1124,6 +1235,16 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& pl, void* worksp
     k.counters = fused ? a.counters : nullptr;
     k.xmap = fused && pl.xmap;
     if (pl.max_splits > kMaxSplits) return hipErrorInvalidValue;
+    if (decode_generic(a.geom.head_dim)) {
+        if (a.geom.head_dim > kGenericMaxDim || pl.split_tokens > kGenericMaxSplitTokens) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(decode_generic_kernel, dim3(pl.max_splits, a.heads, a.nb), dim3(kThreads), 0, stream, k, a.dtype);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        if (after_split && (e = hipEventRecord(after_split, stream)) != hipSuccess) return e;
+        if (pl.max_splits == 1) return hipSuccess;
+        hipLaunchKernelGGL(decode_generic_combine_kernel, dim3(a.heads, a.nb), dim3(kThreads), 0, stream, k);
+        return hipGetLastError();
+    }
     const void* fn;
     if (uses_mfma(a)) {
         const bool bf = a.dtype == QR_DTYPE_BF16;

@@ -117,7 +117,7 @@ hipError_t launch_gather(const GatherArgs& a, hipStream_t stream);
 // dtype and scattered into their pages; q rows of the same positions ([n][q_width],
 // q_width a multiple of head_dim) are rotated in place.  freq[i] = theta^(-2i/D) is
 // computed on the host with the same libm powf as the reference's MathF.Pow path.
-constexpr int kMaxRopeHalf = 128;  // head_dim <= 256
+constexpr int kMaxRopeHalf = 256;  // head_dim <= 512
 struct RopeAppendArgs {
     AppendArgs app;         // src[0] = K, src[1] = V, fp32, row length kv_dim
     float* q;               // may be null
@@ -131,6 +131,9 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t stream);
 // rope_items_per_thread(...) <= kRopeMaxItems.
 constexpr int kRopeThreads = 256;
 constexpr int kRopeMaxItems = 8;
+// Head sizes the item kernels do not take run on a generic per-pair kernel (any position,
+// device-side too).
+inline bool rope_generic(int head_dim) { return head_dim % 8 != 0 || head_dim > 256; }
 inline int rope_items_per_thread(int heads, int head_dim) {
     return (heads * (head_dim / 8) + kRopeThreads - 1) / kRopeThreads;
 }
@@ -143,6 +146,10 @@ hipError_t launch_positions(int* out, const int* pos0_dev, int n, hipStream_t st
 
 // ------------------------------------------------------------------ GQA decode
 constexpr int kMaxDecodeBatch = 64;  // decode entries per launch (descriptor passed by value)
+// Head sizes: the vector and MFMA decode kernels take multiples of 8 from 16 to 256; any
+// other size up to kGenericMaxDim runs on the scalar generic kernel.
+constexpr int kGenericMaxDim = 512;
+inline bool decode_generic(int head_dim) { return head_dim % 8 != 0 || head_dim < 16 || head_dim > 256; }
 
 struct DecodeArgs {
     const void* pool;

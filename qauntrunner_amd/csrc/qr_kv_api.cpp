@@ -233,8 +233,8 @@ int qr_kv_create(qr_kv** out, int layers, int heads, int kv_heads, int head_dim,
     QR_CHECK_ARG(layers >= 1, "layers must be >= 1 (got %d)", layers);
     QR_CHECK_ARG(heads >= 1 && kv_heads >= 1 && kv_heads <= heads,
                  "need 1 <= kv_heads <= heads (got heads=%d kv_heads=%d)", heads, kv_heads);
-    QR_CHECK_ARG(head_dim >= 16 && head_dim <= 256 && head_dim % 8 == 0,
-                 "head_dim %d unsupported (a multiple of 8 from 16 to 256)", head_dim);
+    QR_CHECK_ARG(head_dim >= 1 && head_dim <= kGenericMaxDim, "head_dim %d unsupported (1 to %d)", head_dim,
+                 kGenericMaxDim);
     QR_CHECK_ARG(max_seq >= 1, "max_seq must be >= 1 (got %d)", max_seq);
     QR_CHECK_ARG(dtype_valid(kv_dtype), "unknown kv dtype %d", kv_dtype);
     QR_CHECK_ARG(max_batch >= 1, "max_batch must be >= 1 (got %d)", max_batch);
@@ -698,7 +698,8 @@ int rope_step_dev(qr_kv* kv, int seq_id, int layer, int n, const int* pos_dev, f
     QR_CHECK_ARG(pos_dev && k_dev && v_dev, "null pos/k/v pointer");
     // checked before the page claim is enqueued: a rejected append must leave the
     // device accounting as it was
-    QR_CHECK_ARG(rope_items_per_thread(kv->kv_heads + (q_dev ? kv->heads : 0), kv->head_dim) <= kRopeMaxItems,
+    QR_CHECK_ARG(rope_generic(kv->head_dim) ||
+                     rope_items_per_thread(kv->kv_heads + (q_dev ? kv->heads : 0), kv->head_dim) <= kRopeMaxItems,
                  "device-position RoPE appends take at most %d dims of K and q per position (got %d)",
                  kRopeThreads * kRopeMaxItems * 8, (kv->kv_heads + (q_dev ? kv->heads : 0)) * kv->head_dim);
     DeviceGuard dg(kv->device);

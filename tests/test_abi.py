@@ -36,9 +36,9 @@ def test_version_and_status_names():
 @pytest.mark.parametrize("args,needle", [
     ((0, 8, 2, 64, 512, 0, 1), "layers"),
     ((1, 2, 4, 64, 512, 0, 1), "kv_heads"),
-    ((1, 8, 2, 44, 512, 0, 1), "head_dim"),
-    ((1, 8, 2, 8, 512, 0, 1), "head_dim"),
-    ((1, 8, 2, 264, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 0, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, -3, 512, 0, 1), "head_dim"),
+    ((1, 8, 2, 513, 512, 0, 1), "head_dim"),   # any head size from 1 to 512
     ((1, 8, 2, 64, 0, 0, 1), "max_seq"),
     ((1, 8, 2, 64, 512, 7, 1), "dtype"),
     ((1, 8, 2, 64, 512, 0, 0), "max_batch"),
@@ -90,7 +90,7 @@ def test_null_handles_are_rejected():
 
 def test_status_maps_to_python_exceptions():
     with pytest.raises(qr.QrInvalidArgument):
-        qr.PagedKvCache(1, 8, 2, 44, 512)
+        qr.PagedKvCache(1, 8, 2, 600, 512)  # head_dim above 512
     assert issubclass(qr.QrOutOfRange, IndexError) and issubclass(qr.QrNotResident, LookupError)
 
 
