@@ -135,6 +135,71 @@ __global__ __launch_bounds__(kAbsThreads) void mla_absorb_kernel(MlaProjArgs a) 
     }
 }
 
+// q-absorb of one query with nope <= kAbsSumRows, block formats: workgroup = 4 waves =
+// (128-column slice, head).  Wave w loads rows j = w, w + 4, ... of the head's W_UK, all at
+// once, and lane l writes the products q_j W[h,j,k] of its columns k = 2l, 2l + 1 to LDS;
+// then thread c adds column c's products in row order from 0 -- the reference's sequence,
+// the same bits as the one-wave kernel, whose rows stream in blocks with one block in
+// flight.  Four times the waves carry the block formats' decode: Q8_0 kvb at the C5 shape
+// 9.0 -> 7.9 us; bf16 kvb, whose decode is a shift, 6.6 -> 7.0 us, so the fp formats keep
+// the one-wave form.
+constexpr int kAbsSumRows = 128;
+
+template <int FMT>
+__global__ __launch_bounds__(256) void mla_absorb_sum_kernel(MlaProjArgs a) {
+    constexpr int RPW = kAbsSumRows / 4;  // rows per wave
+    __shared__ float prod[kAbsSumRows][2 * kAbsThreads];
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nope = a.nope;
+    const int qk = nope + a.rope;
+    const float* q = a.in + static_cast<long long>(h) * qk;
+    const int k = 2 * (blockIdx.x * kAbsThreads + lane);
+    const int kk = k < a.kv_lora ? k : 0;  // lanes past the end load a valid column and drop it
+    const uint8_t* W = a.w + static_cast<long long>(h) * (nope + a.vdim) * a.row_bytes;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(W), static_cast<short>(0), static_cast<int>(nope * a.row_bytes), kBufferFlags);
+    const uint32_t rb = static_cast<uint32_t>(a.row_bytes);
+    Raw<FMT> buf[RPW];
+    float qj[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int j = min(w + 4 * i, nope - 1);  // rows past nope: a valid row, not stored
+        buf[i] = raw<FMT>(BufRow{rsrc, j * rb}, kk);
+        qj[i] = q[j];
+    }
+    // every load is issued before the first product (the compiler would otherwise walk
+    // the rows one round trip at a time in a few registers)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int j = w + 4 * i;
+        if (j >= nope) break;
+        const float2 wv = dec<FMT>(buf[i], kk);
+        *reinterpret_cast<float2*>(&prod[j][2 * lane]) = make_float2(mul_rn(qj[i], wv.x), mul_rn(qj[i], wv.y));
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * kAbsThreads) {
+        const int c = threadIdx.x;
+        const int kc = 2 * blockIdx.x * kAbsThreads + c;
+        float acc = 0.0f;
+        int j = 0;
+        for (; j + 16 <= nope; j += 16) {  // 16 reads in flight, then their adds in order
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = prod[j + u][c];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc = add_rn(acc, v[u]);
+        }
+        for (; j < nope; ++j) acc = add_rn(acc, prod[j][c]);
+        if (kc < a.kv_lora) a.out[static_cast<long long>(h) * a.kv_lora + kc] = acc;
+    }
+    if (a.q_rope && blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < a.rope; i += 256) a.q_rope[static_cast<long long>(h) * a.rope + i] = q[nope + i];
+    }
+}
+
 // ------------------------------------------------------------------ W_UV
 // One workgroup per (32 rows of W_UV,h, head, batch tile).  The rows are one contiguous
 // byte range of kvb, taken in column slabs of <= kSlabBytes per row.  A slab is copied
@@ -393,7 +458,10 @@ template <int FMT>
 hipError_t launch_absorb_fmt(const MlaProjArgs& a, hipStream_t stream) {
     const dim3 block(kAbsThreads);
     const int gx = (a.kv_lora / 2 + kAbsThreads - 1) / kAbsThreads;
-    if (a.nq == 1) {
+    constexpr bool fp = FMT == QR_FMT_F32 || FMT == QR_FMT_F16 || FMT == QR_FMT_BF16;
+    if (!fp && a.nq == 1 && a.nope <= kAbsSumRows) {
+        hipLaunchKernelGGL((mla_absorb_sum_kernel<FMT>), dim3(gx, a.heads, 1), dim3(256), 0, stream, a);
+    } else if (a.nq == 1) {
         hipLaunchKernelGGL((mla_absorb_kernel<FMT, 1>), dim3(gx, a.heads, 1), block, 0, stream, a);
     } else {
         hipLaunchKernelGGL((mla_absorb_kernel<FMT, 4>), dim3(gx, a.heads, (a.nq + 3) / 4), block, 0, stream, a);
