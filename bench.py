@@ -606,6 +606,47 @@ def synth_kvb(w, gen, dev):
     return to_cache_bits(x, "f16" if fmt == "F16" else "bf16").view(torch.uint8).reshape(-1)
 
 
+def stream_floor_us(nbytes, steps, warmup):
+    """Average time of a plain streaming read of `nbytes` (libqr_floor.so: every byte read
+    once with non-temporal 16-byte loads, nothing computed), launched back to back over
+    rotated buffers of at least ROTATE_BYTES in all, as the workloads rotate their data; the
+    faster of 256 and 512 workgroups.  What HBM gives a kernel that does nothing but read,
+    on this GPU in this process.  None when the helper library is not built."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "qauntrunner_amd", "libqr_floor.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.qr_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_int, ctypes.c_void_p]
+    n = (int(nbytes) + 4095) // 4096 * 4096
+    sets = max(1, math.ceil(ROTATE_BYTES / n))
+    buf = torch.ones(sets * n, dtype=torch.uint8, device="cuda:0")
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    best = None
+    for blocks in (256, 512):
+        def launch(reps):
+            rc = lib.qr_floor_read(buf.data_ptr(), n, sets, reps, sink.data_ptr(), blocks, stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"qr_floor_read returned {rc}")
+        launch(max(1, warmup))
+        torch.cuda.synchronize()
+        t0.record(stream)
+        launch(steps)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps * nbytes / n
+        best = us if best is None else min(best, us)
+    del buf
+    return best
+
+
 def time_split_kernel(handle, step, first, steps, stream):
     """Average duration of the split-K kernel alone: per step, a HIP event is recorded
     on the launch stream before the call and the library records another right after
@@ -881,6 +922,12 @@ def main():
                 "frac": achieved / (HBM_PEAK_TBS * 1e3), "traffic": None}
     roof["traffic"] = profiled_traffic(args.config)
     roof["kernel_us"] = round(kms * 1e3, 3)
+    if roof["bound"] == "hbm" and w["kind"] != "rope":
+        # the same bytes read by a kernel that does nothing else (rope writes half its bytes)
+        floor = stream_floor_us(roof["achieved"] * 1e9 * kms * 1e-3, args.steps, args.warmup)
+        if floor is not None:
+            roof["stream_floor_us"] = round(floor, 3)
+            roof["floor_frac"] = round(floor / (kms * 1e3), 4)
     roof["kernel"] = ("attention call: split-K kernel + split merge (inside the split-K kernel for decode "
                       "plans whose splits fit one pass of the GPU, else a merge kernel; HIP events around the "
                       "timed steps on the launch stream)" if w["kind"] in ("decode", "chunk", "mla") else
