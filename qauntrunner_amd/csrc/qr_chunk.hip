@@ -7,8 +7,11 @@
 //
 // A row is one (query, query head) pair; the G = heads/kv_heads heads of one kv
 // head and a block of consecutive queries form the rows of a workgroup, so every
-// K/V tile staged in LDS serves them all.  Workgroup = 4 waves x NT x 16 rows; each
-// wave owns its rows for the whole split, so waves never exchange data inside a tile.
+// K/V tile staged in LDS serves them all.  Workgroup = 4 row groups of NT x 16 rows; at
+// NT >= 2 one wave per row group scores every position of a tile; at NT = 1 (a few
+// queries, e.g. speculative verify) two waves per row group take one half of the tile's
+// positions each, so that every SIMD runs two waves, and the halves merge once at the end.
+// Waves never exchange data inside a tile.
 //   QK: S^T[pos][row] = K[pos][dims] . Q^T[dims][row]     (M positions, N rows)
 //   PV: O^T[dim][row] += V^T[dim][pos] . P^T[pos][row]     (M dims,      N rows)
 // Tiles of 64 positions -- two steps of the MFMA operand page layout (qr_kernels.hpp) --
@@ -133,8 +136,8 @@ __device__ __forceinline__ float max_quarters(float x) {
 // QSPLIT: q is not exact in the cache type and enters as hi + lo parts.
 template <bool BF16, int D, int NT, int NSTAGE, bool QSPLIT>
 // Workgroups per CU: two at NT <= 2 with two LDS stages (64 KiB); one with three stages
-// (96 KiB of LDS) or NT = 4 (registers).
-__global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_tile_kernel(const ChunkK p) {
+// (96 KiB of LDS) or NT = 4 (registers).  NT = 1 runs eight waves per workgroup.
+__global__ void __launch_bounds__(NT == 1 ? 512 : 256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_tile_kernel(const ChunkK p) {
     using T = typename std::conditional<BF16, __bf16, _Float16>::type;
     typedef T vec8 __attribute__((ext_vector_type(8)));
     constexpr int NK = D / 32;               // QK k-steps
@@ -142,10 +145,14 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     constexpr int RB = D * 2;                // K row bytes
     constexpr int KB = kTile * RB;           // K tile bytes
     constexpr int VB = D * kTile * 2;        // V^T tile bytes (D rows of 128 bytes)
-    constexpr int KI = KB / 1024 / 4;        // K DMA instructions per wave and tile
-    constexpr int VI = VB / 1024 / 4;        // V DMA instructions per wave and tile
+    constexpr bool PS = NT == 1;             // position halves: two waves per row group
+    constexpr int WAVES = PS ? 8 : 4;
+    constexpr int NMT = PS ? 2 : 4;          // QK M tiles (16 positions) per wave and tile
+    constexpr int NKS = PS ? 1 : 2;          // PV k-steps (32 positions) per wave and tile
+    constexpr int KI = KB / 1024 / WAVES;    // K DMA instructions per wave and tile
+    constexpr int VI = VB / 1024 / WAVES;    // V DMA instructions per wave and tile
     constexpr int PER_TILE = KI + VI;        // vector-memory ops per wave and tile
-    static_assert(KI >= 1 && VI >= 1, "tile must split over 4 waves");
+    static_assert(KI >= 1 && VI >= 1, "tile must split over the waves");
 
     __shared__ __attribute__((aligned(1024))) char lds[NSTAGE][KB + VB];
 
@@ -169,7 +176,9 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     const int qblk = uq < hq ? p.qblocks - 1 - uq : uq - hq;
     const int kvh = unit / (p.splits * p.qblocks);
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & (WAVES - 1);
+    const int rw = PS ? (wave & 3) : wave;  // row group
+    const int ph = PS ? (wave >> 2) : 0;    // position half (NT = 1): the tile's step ph
     const int q4 = lane >> 4;
     const int col = lane & 15;
 
@@ -179,7 +188,7 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
     bool row_on[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        const int rho = wave * 16 * NT + j * 16 + col;
+        const int rho = rw * 16 * NT + j * 16 + col;
         row_q[j] = q_first + (rho >> p.group_shift);
         row_h[j] = kvh * p.group + (rho & (p.group - 1));
         row_on[j] = row_q[j] < p.nq && (rho >> p.group_shift) < p.queries_per_block;
@@ -217,13 +226,13 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
             const_cast<char*>(kbase + p.plane_elems * 2), 0, VB, kBufferFlags);
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            const int n = wave + 4 * i;
+            const int n = wave + WAVES * i;
             if (p.kv_once) buffer_load_lds16<kCacheNt>(rk, dst + 1024 * n, lane16, 1024 * n);
             else buffer_load_lds16(rk, dst + 1024 * n, lane16, 1024 * n);
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int n = wave + 4 * i;
+            const int n = wave + WAVES * i;
             if (p.kv_once) buffer_load_lds16<kCacheNt>(rv, dst + KB + 1024 * n, lane16, 1024 * n);
             else buffer_load_lds16(rv, dst + KB + 1024 * n, lane16, 1024 * n);
         }
@@ -299,7 +308,7 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
             // the last tile: clear V past the end.  16-byte chunk c of the V tile (step
             // c / (NDT 64), dim tile, lane L = c % 64) holds positions 32 step + 8 (L / 16)
             // .. + 7 of one dim.
-            for (int c = threadIdx.x; c < 2 * NDT * 64; c += 256) {
+            for (int c = threadIdx.x; c < 2 * NDT * 64; c += 64 * WAVES) {
                 const int pb = 32 * (c / (NDT * 64)) + 8 * ((c & 63) >> 4);
                 if (pb + 8 <= nvalid) continue;
                 uint32_t* w = reinterpret_cast<uint32_t*>(const_cast<char*>(vt) + 16 * c);
@@ -310,12 +319,13 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
             lds_barrier();
         }
 
-        // ---- QK
-        f32x4_t sc[NT][4];
+        // ---- QK (M tiles mt0 .. mt0 + NMT - 1 of the tile)
+        const int mt0 = PS ? 2 * ph : 0;
+        f32x4_t sc[NT][NMT];
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) sc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int lm = 0; lm < NMT; ++lm) sc[j][lm] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         // The K operands of M tile mt+1 are read before the MFMAs of M tile mt (scheduling
         // barriers keep the compiler from sinking each read next to its first use, where
         // every MFMA pair waited out an LDS round trip).
@@ -326,17 +336,17 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
 #pragma unroll
                 for (int kk = 0; kk < NK; ++kk) dst[kk] = *reinterpret_cast<const vec8*>(op + 1024 * kk);
             };
-            kread(0, ka[0]);
+            kread(mt0, ka[0]);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                if (mt + 1 < 4) kread(mt + 1, ka[(mt + 1) & 1]);
+            for (int lm = 0; lm < NMT; ++lm) {
+                if (lm + 1 < NMT) kread(mt0 + lm + 1, ka[(lm + 1) & 1]);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
                     for (int j = 0; j < NT; ++j) {
-                        sc[j][mt] = mfma16(ka[mt & 1][kk], qhi[j][kk], sc[j][mt]);
-                        if (QSPLIT) sc[j][mt] = mfma16(ka[mt & 1][kk], qlo[j][kk], sc[j][mt]);
+                        sc[j][lm] = mfma16(ka[lm & 1][kk], qhi[j][kk], sc[j][lm]);
+                        if (QSPLIT) sc[j][lm] = mfma16(ka[lm & 1][kk], qlo[j][kk], sc[j][lm]);
                     }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -349,11 +359,12 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
             for (int j = 0; j < NT; ++j) {
                 const int lim = min(t_end - 1, pos0 + row_q[j]);  // last position row j sees
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
+                for (int lm = 0; lm < NMT; ++lm)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        const int mt = mt0 + lm;
                         const int tok = t0 + 32 * (mt >> 1) + 8 * q4 + 4 * (mt & 1) + r;
-                        sc[j][mt][r] = tok <= lim ? sc[j][mt][r] : -INFINITY;
+                        sc[j][lm][r] = tok <= lim ? sc[j][lm][r] : -INFINITY;
                     }
             }
         }
@@ -366,13 +377,21 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             // the lane's 16 scores: five v_max3 over 15 of them, two more over those five
-            // and the last, one v_max; then the other lane quarters
-            const float a0 = max3f(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
-            const float a1 = max3f(sc[j][0][3], sc[j][1][0], sc[j][1][1]);
-            const float a2 = max3f(sc[j][1][2], sc[j][1][3], sc[j][2][0]);
-            const float a3 = max3f(sc[j][2][1], sc[j][2][2], sc[j][2][3]);
-            const float a4 = max3f(sc[j][3][0], sc[j][3][1], sc[j][3][2]);
-            const float tmax = max_quarters(max2f(max3f(a0, a1, a2), max3f(a3, a4, sc[j][3][3])));
+            // and the last, one v_max (8 scores at NT = 1: three v_max3, one v_max); then
+            // the other lane quarters
+            float tmax;
+            if constexpr (NMT == 4) {
+                const float a0 = max3f(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
+                const float a1 = max3f(sc[j][0][3], sc[j][1][0], sc[j][1][1]);
+                const float a2 = max3f(sc[j][1][2], sc[j][1][3], sc[j][2][0]);
+                const float a3 = max3f(sc[j][2][1], sc[j][2][2], sc[j][2][3]);
+                const float a4 = max3f(sc[j][3][0], sc[j][3][1], sc[j][3][2]);
+                tmax = max_quarters(max2f(max3f(a0, a1, a2), max3f(a3, a4, sc[j][3][3])));
+            } else {
+                const float a0 = max3f(sc[j][0][0], sc[j][0][1], sc[j][0][2]);
+                const float a1 = max3f(sc[j][0][3], sc[j][1][0], sc[j][1][1]);
+                tmax = max_quarters(max3f(a0, a1, max2f(sc[j][1][2], sc[j][1][3])));
+            }
             ts[j] = tmax * sscale[j];
             grow[j] = ts[j] > m[j] + 8.f;
             any_rescale |= grow[j] && m[j] != -INFINITY;
@@ -386,35 +405,65 @@ __global__ void __launch_bounds__(256, NT <= 2 && NSTAGE <= 2 ? 2 : 1) chunk_til
                 for (int t = 0; t < NDT; ++t) acc[j][t] *= corr;
             }
         }
-        vec8 pb[NT][2];
+        vec8 pb[NT][NKS];
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             if (grow[j]) m[j] = ts[j];
             const float mneg = m[j] == -INFINITY ? 0.f : -m[j];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
+            for (int lm = 0; lm < NMT; ++lm)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    pb[j][mt >> 1][4 * (mt & 1) + r] = static_cast<T>(fast_exp2(fmaf(sc[j][mt][r], sscale[j], mneg)));
+                    pb[j][lm >> 1][4 * (lm & 1) + r] = static_cast<T>(fast_exp2(fmaf(sc[j][lm][r], sscale[j], mneg)));
         }
 
         // ---- PV (and the row sums: a ones operand turns the MFMA into sum over positions).
         // Every V^T operand of a k-slot half is read before its MFMAs (a scheduling barrier
         // keeps the reads ahead), so the later reads land while the first MFMAs run.
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int kq = 0; kq < NKS; ++kq) {
+            const int ks = PS ? ph : kq;
             vec8 va[NDT];
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
                 va[dt] = *reinterpret_cast<const vec8*>(vt + SB * ks + 1024 * dt + 16 * lane);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < NT; ++j) accl[j] = mfma16(ones, pb[j][ks], accl[j]);
+            for (int j = 0; j < NT; ++j) accl[j] = mfma16(ones, pb[j][kq], accl[j]);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                for (int j = 0; j < NT; ++j) acc[j][dt] = mfma16(va[dt], pb[j][ks], acc[j][dt]);
+                for (int j = 0; j < NT; ++j) acc[j][dt] = mfma16(va[dt], pb[j][kq], acc[j][dt]);
         }
+    }
+
+    if constexpr (PS) {
+        // The position halves of each row group merge: waves 4-7 hand (m, l, o) to waves
+        // 0-3 through LDS stages 0 and 1 (free once every wave is past the last tile), lane
+        // for lane in the accumulators' own layout.  (The tile buffers stay the kernel's
+        // only LDS object: with a second one the compiler waited for every tile copy in
+        // flight before each tile's first operand read.)
+        static_assert(NSTAGE >= 2 && 4 * NDT * 64 * 16 <= KB + VB, "the handed-over rows fit stage 0");
+        f32x4_t* xo = reinterpret_cast<f32x4_t*>(lds[0]) + (rw * NDT) * 64 + lane;
+        float* xm = reinterpret_cast<float*>(lds[1]) + rw * 64 + lane;  // [4][64], then l
+        float* xl = xm + 4 * 64;
+        lds_barrier();
+        if (ph == 1) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) xo[dt * 64] = acc[0][dt];
+            *xm = m[0];
+            *xl = accl[0][0];
+        }
+        lds_barrier();
+        if (ph == 1) return;
+        const float m1 = *xm;
+        const float M = fmaxf(m[0], m1);
+        const float c0 = m[0] == -INFINITY ? 0.f : fast_exp2(m[0] - M);
+        const float c1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - M);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[0][dt] = acc[0][dt] * c0 + xo[dt * 64] * c1;
+        accl[0][0] = accl[0][0] * c0 + *xl * c1;
+        m[0] = M;
     }
 
 #pragma unroll
@@ -485,11 +534,11 @@ hipError_t launch_q(const ChunkK& k, bool qsplit, dim3 grid, hipStream_t s) {
         if (qsplit) return hipErrorInvalidValue;
     } else {
         if (qsplit) {
-            hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, true>), grid, dim3(256), 0, s, k);
+            hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, true>), grid, dim3(NT == 1 ? 512 : 256), 0, s, k);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, false>), grid, dim3(256), 0, s, k);
+    hipLaunchKernelGGL((chunk_tile_kernel<BF, D, NT, NSTAGE, false>), grid, dim3(NT == 1 ? 512 : 256), 0, s, k);
     return hipGetLastError();
 }
 
