@@ -110,6 +110,11 @@ def test_c4_speculative_verify_fp16(gpu):
     ("bf16", 32, 8, 128, 4000, 300, "f32"),  # fp32 queries as hi + lo bf16, two N tiles
     ("bf16", 8, 2, 64, 130, 1000, "f16"),    # fp16 queries into a bf16 cache, four N tiles
     ("f16", 16, 2, 128, 70000, 5, "f16"),    # few queries over a long cache: split-K, 3 stages
+    # verify-sized blocks (one N tile: two waves per row group, one per 32-position half)
+    ("f16", 64, 8, 64, 20, 8, "f32"),        # one tile of 28 positions: the second half all masked
+                                             # (fp16: over 21 keys bf16's 8-bit P alone errs ~1.6e-3)
+    ("f16", 32, 8, 128, 40, 8, "f16"),       # one tile of 48: the drafts' causal edge in the second half
+    ("bf16", 64, 8, 128, 100, 8, "bf16"),    # two tiles, the last one partial
 ])
 def test_chunk_mfma_shapes(gpu, dtype, heads, kv_heads, D, pos0, nq, q_dtype):
     n = pos0 + nq
