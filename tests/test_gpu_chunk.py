@@ -115,6 +115,7 @@ def test_c4_speculative_verify_fp16(gpu):
                                              # (fp16: over 21 keys bf16's 8-bit P alone errs ~1.6e-3)
     ("f16", 32, 8, 128, 40, 8, "f16"),       # one tile of 48: the drafts' causal edge in the second half
     ("bf16", 64, 8, 128, 100, 8, "bf16"),    # two tiles, the last one partial
+    ("bf16", 64, 8, 128, 5000, 8, "f32"),    # fp32 drafts as hi + lo bf16 over split keys
 ])
 def test_chunk_mfma_shapes(gpu, dtype, heads, kv_heads, D, pos0, nq, q_dtype):
     n = pos0 + nq
